@@ -1,0 +1,67 @@
+/* Extensions of this MI355X build that have no counterpart in the reference API. */
+#ifndef VKLLM_HIP_H
+#define VKLLM_HIP_H
+#include <stdint.h>
+#include "vkllm_errors.h"
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+struct vkllm_context;
+struct vkllm_graph;
+struct vkllm_models_llama2;
+
+/* How graphs built by vkllm_models_llama2_build_graph execute:
+ * VKLLM_EXEC_FUSED (default): the whole token step as fused kernels; S == 1 steps replay a captured hipGraph.
+ * VKLLM_EXEC_NODES: node by node through the VKLLM_OP_* kernels, every intermediate tensor materialised.
+ * The environment variable VKLLM_EXEC=nodes|fused sets the initial mode of a context. */
+#define VKLLM_EXEC_FUSED 0
+#define VKLLM_EXEC_NODES 1
+extern vkllm_err_t vkllm_hip_set_exec_mode(struct vkllm_context *context, int mode);
+extern int vkllm_hip_get_exec_mode(struct vkllm_context *context);
+
+/* 1: capture S == 1 fused steps into a hipGraph and replay it (default); 0: launch kernels directly */
+extern vkllm_err_t vkllm_hip_set_graph_replay(struct vkllm_context *context, int enable);
+
+/* per-launch hipEvent timing feeding vkllm_pipeline_query_exec_time and context->stats (also VKLLM_TIMING=1) */
+extern vkllm_err_t vkllm_hip_set_timing(struct vkllm_context *context, int enable);
+
+/* Model configuration for vkllm_models_llama2_init_random. */
+struct vkllm_llama2_config
+{
+    uint32_t block_count;
+    uint32_t embedding_length;
+    uint32_t head_count;
+    uint32_t feed_forward_length;
+    uint32_t vocab_size;
+    uint32_t context_length;
+    float layer_norm_rms_epsilon;
+    float rope_freq_base;
+    float weight_std;
+};
+
+/* Builds a LLaMA-2 model whose weights are generated on the GPU from (config, seed) by the same definition the
+ * oracle's random-init GGUF writer uses (Irwin-Hall normal of counter-based SplitMix64 words, times
+ * weight_std, rounded to fp16; norm weights 1.0), so it equals loading that GGUF file, without the file.
+ * Tokenizer metadata is left empty. */
+extern vkllm_err_t vkllm_models_llama2_init_random(struct vkllm_context *context, struct vkllm_models_llama2 *model,
+                                                   const struct vkllm_llama2_config *config, uint64_t seed);
+
+/* Copies the fp16 logits [rows, vocab] of the model's last fused step into dst (rows <= that step's S). */
+extern vkllm_err_t vkllm_hip_model_last_logits(struct vkllm_context *context, struct vkllm_models_llama2 *model,
+                                               uint16_t *dst, uint32_t rows);
+
+/* Synchronise the context's stream. */
+extern vkllm_err_t vkllm_hip_synchronize(struct vkllm_context *context);
+
+/* Name of the device (hipDeviceProp_t::gcnArchName) for logs. */
+extern const char *vkllm_hip_device_arch(struct vkllm_context *context);
+
+/* Layout facts for FFI bindings: sizeof and field offsets of the public structs. Returns the number of
+ * entries written (at most n); `names` receives static strings. */
+extern int vkllm_hip_abi_layout(const char **names, uint64_t *values, int n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,523 @@
+/*
+ * CPU oracle: operators. TEST INFRASTRUCTURE ONLY -- see oracle.h.
+ * Each function restates the semantics of one reference operator; citations are to the vkllm.c tree.
+ */
+#include "oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* fp16 conversions: IEEE binary16 with round-to-nearest-even, which is what GPU conversion instructions do. The
+ * reference's own host helper (src/core/vkllm_common.h:157-186) truncates, but it only prepares test inputs;
+ * device-side conversions in the shaders round to nearest. */
+uint16_t oracle_f32_to_f16(float f)
+{
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t exp = (x >> 23) & 0xffu;
+    uint32_t mant = x & 0x7fffffu;
+    if (exp == 0xffu)
+    {
+        if (mant)
+            return (uint16_t)(sign | 0x7e00u | (mant >> 13));
+        return (uint16_t)(sign | 0x7c00u);
+    }
+    int e = (int)exp - 127 + 15;
+    if (e >= 31)
+        return (uint16_t)(sign | 0x7c00u);
+    if (e <= 0)
+    {
+        if (e < -10)
+            return (uint16_t)sign;
+        uint32_t full = mant | 0x800000u;
+        int shift = 14 - e;
+        uint32_t m = full >> shift;
+        uint32_t rem = full & ((1u << shift) - 1u);
+        uint32_t halfway = 1u << (shift - 1);
+        if (rem > halfway || (rem == halfway && (m & 1u)))
+            m++;
+        return (uint16_t)(sign | m);
+    }
+    uint32_t h = sign | ((uint32_t)e << 10) | (mant >> 13);
+    uint32_t rem = mant & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u)))
+        h++;
+    return (uint16_t)h;
+}
+
+float oracle_f16_to_f32(uint16_t h)
+{
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t exp = ((uint32_t)h >> 10) & 0x1fu;
+    uint32_t mant = (uint32_t)h & 0x3ffu;
+    uint32_t x;
+    if (exp == 0)
+    {
+        if (mant == 0)
+            x = sign;
+        else
+        {
+            int s = 0;
+            while (!(mant & 0x400u))
+            {
+                mant <<= 1;
+                s++;
+            }
+            mant &= 0x3ffu;
+            x = sign | ((uint32_t)(127 - 14 - s) << 23) | (mant << 13);
+        }
+    }
+    else if (exp == 31)
+        x = sign | 0x7f800000u | (mant << 13);
+    else
+        x = sign | ((exp + 112u) << 23) | (mant << 13);
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* synthetic inputs */
+#define GOLDEN 0x9E3779B97F4A7C15ull
+
+uint64_t oracle_splitmix64(uint64_t stream, uint64_t n)
+{
+    uint64_t z = stream + (n + 1) * GOLDEN;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+float oracle_normal(uint64_t stream, uint64_t i)
+{
+    int32_t sum = 0;
+    for (int r = 0; r < 3; ++r)
+    {
+        uint64_t v = oracle_splitmix64(stream, 3 * i + (uint64_t)r);
+        for (int k = 0; k < 4; ++k)
+            sum += (int32_t)((v >> (16 * k)) & 0xffffu);
+    }
+    return (float)(sum + 6 - 6 * 65536) / 65536.0f;
+}
+
+uint64_t oracle_tensor_stream(uint64_t seed, uint32_t tensor_id)
+{
+    return oracle_splitmix64(seed, tensor_id);
+}
+
+uint16_t oracle_weight_f16(uint64_t seed, uint32_t tensor_id, uint64_t i, float std)
+{
+    float z = oracle_normal(oracle_tensor_stream(seed, tensor_id), i);
+    return oracle_f32_to_f16(z * std);
+}
+
+uint32_t oracle_prompt_token(uint64_t seed, uint32_t i, uint32_t vocab)
+{
+    return (uint32_t)(oracle_splitmix64(seed, i) % vocab);
+}
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* element access */
+static inline size_t off4(const oracle_tensor *t, uint32_t b, uint32_t c, uint32_t h, uint32_t w)
+{
+    return (size_t)b * t->strides[0] + (size_t)c * t->strides[1] + (size_t)h * t->strides[2] +
+           (size_t)w * t->strides[3];
+}
+
+static inline float rd(const oracle_tensor *t, size_t off)
+{
+    switch (t->dtype)
+    {
+    case ORACLE_F32:
+        return ((const float *)t->data)[off];
+    case ORACLE_F16:
+        return oracle_f16_to_f32(((const uint16_t *)t->data)[off]);
+    case ORACLE_U32:
+        return (float)((const uint32_t *)t->data)[off];
+    case ORACLE_I8:
+        return (float)((const int8_t *)t->data)[off];
+    }
+    return 0.0f;
+}
+
+static inline void wr(oracle_tensor *t, size_t off, float v)
+{
+    switch (t->dtype)
+    {
+    case ORACLE_F32:
+        ((float *)t->data)[off] = v;
+        break;
+    case ORACLE_F16:
+        ((uint16_t *)t->data)[off] = oracle_f32_to_f16(v);
+        break;
+    case ORACLE_U32:
+        ((uint32_t *)t->data)[off] = (uint32_t)v;
+        break;
+    case ORACLE_I8:
+        ((int8_t *)t->data)[off] = (int8_t)v;
+        break;
+    }
+}
+
+static inline size_t esize(int dtype)
+{
+    return dtype == ORACLE_F32 || dtype == ORACLE_U32 ? 4 : dtype == ORACLE_F16 ? 2 : 1;
+}
+
+static inline uint32_t bcast(uint32_t dim, uint32_t i)
+{
+    return dim == 1 ? 0 : i;
+}
+
+static inline float silu(float v)
+{
+    return v / (1.0f + expf(-v));
+}
+
+/* ------------------------------------------------------------------------------------------------------------ */
+/* src/core/vkllm_op_matmul.c:14-24 */
+int oracle_is_transposed_b(const oracle_tensor *a, const oracle_tensor *b, const oracle_tensor *out)
+{
+    uint32_t M = out->shapes[2], N = out->shapes[3], K = a->shapes[3];
+    return a->shapes[2] == M && b->shapes[2] == N && a->shapes[3] == K && b->shapes[3] == K;
+}
+
+/* The broadcast rule of src/core/vkllm_op_matmul.c:37-63 (boardcast_type) reads an operand's batch/channel
+ * stride only where that operand's dimension is not 1, which for operands whose dims are 1 or equal to the
+ * output's is numpy broadcasting. The GEMV path (src/shaders/vkllm_mat_mul_vec.comp:127-165) honours all strides;
+ * the GEMM path (src/shaders/vkllm_matmul_t1.comp:161,178,242) assumes unit stride along W. The oracle honours
+ * all strides. */
+int oracle_matmul(const oracle_tensor *a, const oracle_tensor *b, oracle_tensor *out, float scale, int32_t act)
+{
+    int tb = oracle_is_transposed_b(a, b, out);
+    uint32_t M = out->shapes[2], N = out->shapes[3], K = a->shapes[3];
+    if (a->shapes[2] != M)
+        return -1;
+    if (!tb && !(b->shapes[3] == N && b->shapes[2] == K))
+        return -1;
+    for (int d = 0; d < 2; ++d)
+    {
+        if (a->shapes[d] != 1 && a->shapes[d] != out->shapes[d])
+            return -1;
+        if (b->shapes[d] != 1 && b->shapes[d] != out->shapes[d])
+            return -1;
+    }
+    for (uint32_t bi = 0; bi < out->shapes[0]; ++bi)
+        for (uint32_t ci = 0; ci < out->shapes[1]; ++ci)
+        {
+            uint32_t ab = bcast(a->shapes[0], bi), ac = bcast(a->shapes[1], ci);
+            uint32_t bb = bcast(b->shapes[0], bi), bc = bcast(b->shapes[1], ci);
+            for (uint32_t m = 0; m < M; ++m)
+                for (uint32_t n = 0; n < N; ++n)
+                {
+                    double acc = 0.0;
+                    for (uint32_t k = 0; k < K; ++k)
+                    {
+                        double x = rd(a, off4(a, ab, ac, m, k));
+                        double y = tb ? rd(b, off4(b, bb, bc, n, k)) : rd(b, off4(b, bb, bc, k, n));
+                        acc += x * y;
+                    }
+                    float v = (float)acc * scale;
+                    if (act == 1)
+                        v = silu(v);
+                    wr(out, off4(out, bi, ci, m, n), v);
+                }
+        }
+    return 0;
+}
+
+/* src/core/vkllm_op_embedding.c:40-55 (checks) and src/shaders/vkllm_embedding.comp:138-167: one output row per
+ * index; an index >= the table's row count reads row `unk_tok`. The output row offset is
+ * c*out.strides[0] + h*out.strides[1] + w*out.strides[2] (the shader's index shift, which for the [1,1,1,S]
+ * index tensor of the model is row w). */
+int oracle_embedding(const oracle_tensor *idx, const oracle_tensor *table, oracle_tensor *out, uint32_t unk_tok)
+{
+    if (idx->dtype != ORACLE_U32 || idx->shapes[0] != 1 || table->shapes[0] != 1 || table->shapes[1] != 1)
+        return -1;
+    uint32_t V = table->shapes[2], D = table->shapes[3];
+    for (uint32_t c = 0; c < idx->shapes[1]; ++c)
+        for (uint32_t h = 0; h < idx->shapes[2]; ++h)
+            for (uint32_t w = 0; w < idx->shapes[3]; ++w)
+            {
+                uint32_t tok = ((const uint32_t *)idx->data)[off4(idx, 0, c, h, w)];
+                if (tok >= V)
+                    tok = unk_tok;
+                size_t o = (size_t)c * out->strides[0] + (size_t)h * out->strides[1] + (size_t)w * out->strides[2];
+                size_t p = (size_t)tok * table->strides[2];
+                for (uint32_t i = 0; i < D; ++i)
+                    wr(out, o + i, rd(table, p + i));
+            }
+    return 0;
+}
+
+/* src/core/vkllm_op_rmsnorm.c:27-49 (checks) and src/shaders/vkllm_rmsnorm.comp:31-82:
+ * alpha = 1/sqrt(sum(x^2)/W + eps); y = (x * w) * alpha. Rows are addressed with the input's strides for both
+ * input and output, unit stride along W. */
+int oracle_rmsnorm(const oracle_tensor *x, const oracle_tensor *w, oracle_tensor *out, float eps)
+{
+    for (int d = 0; d < 4; ++d)
+        if (x->shapes[d] != out->shapes[d])
+            return -1;
+    if (w->shapes[0] != 1 || w->shapes[1] != 1 || w->shapes[2] != 1 || w->shapes[3] != x->shapes[3])
+        return -1;
+    uint32_t W = x->shapes[3];
+    for (uint32_t b = 0; b < x->shapes[0]; ++b)
+        for (uint32_t c = 0; c < x->shapes[1]; ++c)
+            for (uint32_t h = 0; h < x->shapes[2]; ++h)
+            {
+                size_t row = off4(x, b, c, h, 0);
+                double ss = 0.0;
+                for (uint32_t i = 0; i < W; ++i)
+                {
+                    double v = rd(x, row + i);
+                    ss += v * v;
+                }
+                float mean = (float)ss / (float)W;
+                float alpha = 1.0f / sqrtf(mean + eps);
+                for (uint32_t i = 0; i < W; ++i)
+                {
+                    float v0 = rd(x, row + i);
+                    float v1 = rd(w, i);
+                    wr(out, row + i, (v0 * v1) * alpha);
+                }
+            }
+    return 0;
+}
+
+void oracle_rope_freqs(float base, uint32_t D, float *freqs)
+{
+    for (uint32_t w = 0; w < D / 2; ++w)
+        freqs[w] = powf(base, (float)(2 * w) / (float)D);
+}
+
+/* src/core/vkllm_op_rope.c:40-58 (checks), src/shaders/vkllm_rope.comp:39-79:
+ * pair (2w, 2w+1) (or (w, w+D/2) in NeoX style) at row h is rotated by f = (offset + h) / base^(2w/D):
+ * (cos f * v0 - sin f * v1, sin f * v0 + cos f * v1). */
+int oracle_rope(const oracle_tensor *in, oracle_tensor *out, uint32_t offset, float base, int neox_style)
+{
+    for (int d = 0; d < 4; ++d)
+        if (in->shapes[d] != out->shapes[d])
+            return -1;
+    uint32_t D = in->shapes[3];
+    float *freqs = (float *)malloc(sizeof(float) * (D / 2 + 1));
+    oracle_rope_freqs(base, D, freqs);
+    for (uint32_t b = 0; b < in->shapes[0]; ++b)
+        for (uint32_t c = 0; c < in->shapes[1]; ++c)
+            for (uint32_t h = 0; h < in->shapes[2]; ++h)
+                for (uint32_t w = 0; 2 * w < D; ++w)
+                {
+                    size_t i0, i1, o0, o1;
+                    if (neox_style)
+                    {
+                        i0 = off4(in, b, c, h, w);
+                        i1 = i0 + (size_t)in->strides[3] * D / 2;
+                        o0 = off4(out, b, c, h, w);
+                        o1 = o0 + (size_t)out->strides[3] * out->shapes[3] / 2;
+                    }
+                    else
+                    {
+                        i0 = off4(in, b, c, h, 2 * w);
+                        i1 = i0 + in->strides[3];
+                        o0 = off4(out, b, c, h, 2 * w);
+                        o1 = o0 + out->strides[3];
+                    }
+                    float f = (float)(offset + h) / freqs[w];
+                    float fc = cosf(f), fs = sinf(f);
+                    float v0 = rd(in, i0), v1 = rd(in, i1);
+                    float q0 = fc * v0 - fs * v1;
+                    float q1 = fs * v0 + fc * v1;
+                    wr(out, o0, q0);
+                    wr(out, o1, q1);
+                }
+    free(freqs);
+    return 0;
+}
+
+/* src/core/vkllm_op_softmax.c:42-60 (checks), src/shaders/vkllm_softmax.comp:42-96: the max is taken over the
+ * whole row; with seq_mask > 0, entries i > h + offsets are left out of the sum and written as 0. Input and
+ * output rows are both addressed with the output's strides, unit stride along W. */
+int oracle_softmax(const oracle_tensor *in, oracle_tensor *out, int32_t seq_mask, uint32_t offsets)
+{
+    for (int d = 0; d < 4; ++d)
+        if (in->shapes[d] != out->shapes[d])
+            return -1;
+    uint32_t W = out->shapes[3];
+    for (uint32_t b = 0; b < out->shapes[0]; ++b)
+        for (uint32_t c = 0; c < out->shapes[1]; ++c)
+            for (uint32_t h = 0; h < out->shapes[2]; ++h)
+            {
+                size_t row = (size_t)b * out->strides[0] + (size_t)c * out->strides[1] + (size_t)h * out->strides[2];
+                float mx = rd(in, row);
+                for (uint32_t i = 0; i < W; ++i)
+                {
+                    float v = rd(in, row + i);
+                    mx = v > mx ? v : mx;
+                }
+                double sum = 0.0;
+                for (uint32_t i = 0; i < W; ++i)
+                {
+                    if (seq_mask > 0 && i > h + offsets)
+                        continue;
+                    sum += expf(rd(in, row + i) - mx);
+                }
+                float s = (float)sum;
+                for (uint32_t i = 0; i < W; ++i)
+                {
+                    if (seq_mask > 0 && i > h + offsets)
+                        wr(out, row + i, 0.0f);
+                    else
+                        wr(out, row + i, expf(rd(in, row + i) - mx) / s);
+                }
+            }
+    return 0;
+}
+
+/* src/core/vkllm_op_update_rows.c:35-56 (checks), src/shaders/vkllm_update_rows.comp:21-46 */
+int oracle_update_rows(const oracle_tensor *src, oracle_tensor *cache, uint32_t offset_rows)
+{
+    if (src->shapes[0] != cache->shapes[0] || src->shapes[1] != cache->shapes[1] ||
+        src->shapes[3] != cache->shapes[3] || offset_rows + src->shapes[2] > cache->shapes[2])
+        return -1;
+    size_t es = esize(src->dtype);
+    for (uint32_t b = 0; b < src->shapes[0]; ++b)
+        for (uint32_t c = 0; c < src->shapes[1]; ++c)
+            for (uint32_t h = 0; h < src->shapes[2]; ++h)
+                for (uint32_t w = 0; w < src->shapes[3]; ++w)
+                    memcpy((char *)cache->data + off4(cache, b, c, h + offset_rows, w) * es,
+                           (const char *)src->data + off4(src, b, c, h, w) * es, es);
+    return 0;
+}
+
+/* src/core/vkllm_op_copy.c:11-30 (checks), src/shaders/vkllm_copy.comp:35-50 */
+int oracle_copy(const oracle_tensor *in, oracle_tensor *out)
+{
+    for (int d = 0; d < 4; ++d)
+        if (in->shapes[d] != out->shapes[d])
+            return -1;
+    if (in->dtype != out->dtype)
+        return -1;
+    size_t es = esize(in->dtype);
+    for (uint32_t b = 0; b < in->shapes[0]; ++b)
+        for (uint32_t c = 0; c < in->shapes[1]; ++c)
+            for (uint32_t h = 0; h < in->shapes[2]; ++h)
+                for (uint32_t w = 0; w < in->shapes[3]; ++w)
+                    memcpy((char *)out->data + off4(out, b, c, h, w) * es,
+                           (const char *)in->data + off4(in, b, c, h, w) * es, es);
+    return 0;
+}
+
+/* src/core/vkllm_op_bin.c (init checks all four shapes equal), src/shaders/vkllm_bin_op.comp:41-73: the
+ * result is computed in fp32 and every tensor is addressed with the output's strides. */
+int oracle_bin(const oracle_tensor *a, const oracle_tensor *b, oracle_tensor *out, int32_t op)
+{
+    for (int d = 0; d < 4; ++d)
+        if (a->shapes[d] != out->shapes[d] || b->shapes[d] != out->shapes[d])
+            return -1;
+    if (op < 0 || op > 3)
+        return -1;
+    for (uint32_t bi = 0; bi < out->shapes[0]; ++bi)
+        for (uint32_t c = 0; c < out->shapes[1]; ++c)
+            for (uint32_t h = 0; h < out->shapes[2]; ++h)
+                for (uint32_t w = 0; w < out->shapes[3]; ++w)
+                {
+                    size_t o = off4(out, bi, c, h, w);
+                    float x = rd(a, o), y = rd(b, o), r;
+                    switch (op)
+                    {
+                    case 0:
+                        r = x + y;
+                        break;
+                    case 1:
+                        r = x - y;
+                        break;
+                    case 2:
+                        r = x * y;
+                        break;
+                    default:
+                        r = x / y;
+                        break;
+                    }
+                    wr(out, o, r);
+                }
+    return 0;
+}
+
+/* src/core/vkllm_op_arg_max.c (checks: same B,C,H; output W == 1, uint32), src/shaders/vkllm_arg_max.comp:40-97:
+ * lane l in [0,32) starts from element l (or -FLT_MAX with index l when l >= W) and scans l+32, l+64, ... with a
+ * strict '>'; then lanes l < s take lane l+s's pair when strictly greater, for s = 16, 8, 4, 2, 1. */
+int oracle_arg_max(const oracle_tensor *in, oracle_tensor *out)
+{
+    if (in->shapes[0] != out->shapes[0] || in->shapes[1] != out->shapes[1] || in->shapes[2] != out->shapes[2] ||
+        out->shapes[3] != 1 || out->dtype != ORACLE_U32)
+        return -1;
+    uint32_t W = in->shapes[3];
+    for (uint32_t b = 0; b < in->shapes[0]; ++b)
+        for (uint32_t c = 0; c < in->shapes[1]; ++c)
+            for (uint32_t h = 0; h < in->shapes[2]; ++h)
+            {
+                size_t row = (size_t)b * in->strides[0] + (size_t)c * in->strides[1] + (size_t)h * in->strides[2];
+                float vals[32];
+                uint32_t idx[32];
+                for (uint32_t l = 0; l < 32; ++l)
+                {
+                    float mv = -FLT_MAX;
+                    uint32_t mi = l;
+                    if (l < W)
+                        mv = rd(in, row + l);
+                    for (uint32_t i = l + 32; i < W; i += 32)
+                    {
+                        float v = rd(in, row + i);
+                        if (v > mv)
+                        {
+                            mv = v;
+                            mi = i;
+                        }
+                    }
+                    vals[l] = mv;
+                    idx[l] = mi;
+                }
+                for (uint32_t s = 16; s > 0; s >>= 1)
+                    for (uint32_t l = 0; l < s; ++l)
+                        if (vals[l + s] > vals[l])
+                        {
+                            vals[l] = vals[l + s];
+                            idx[l] = idx[l + s];
+                        }
+                size_t o = (size_t)b * out->strides[0] + (size_t)c * out->strides[1] + (size_t)h * out->strides[2];
+                ((uint32_t *)out->data)[o] = idx[0];
+            }
+    return 0;
+}
+
+/* src/shaders/vkllm_ffn_up_and_gate.comp:44-149: u = x.Wu[n], g = x.Wg[n] (fp32 accumulation),
+ * out = u * g / (1 + exp(-g)). x [B,C,M,K], Wu/Wg [1,1,N,K], out [B,C,M,N]. The reference host pushes byte
+ * strides to a shader that indexes elements (src/core/vkllm_op_ffn_up_and_gate.c:135-138) and addresses the
+ * output with the input's batch offset; the oracle states the intended element-stride semantics. */
+int oracle_ffn_up_and_gate(const oracle_tensor *x, const oracle_tensor *wu, const oracle_tensor *wg,
+                           oracle_tensor *out)
+{
+    uint32_t K = x->shapes[3], N = wu->shapes[2], M = x->shapes[2];
+    if (wu->shapes[3] != K || wg->shapes[3] != K || wg->shapes[2] != N || out->shapes[2] != M ||
+        out->shapes[3] != N || out->shapes[0] != x->shapes[0] || out->shapes[1] != x->shapes[1])
+        return -1;
+    for (uint32_t b = 0; b < x->shapes[0]; ++b)
+        for (uint32_t c = 0; c < x->shapes[1]; ++c)
+            for (uint32_t m = 0; m < M; ++m)
+                for (uint32_t n = 0; n < N; ++n)
+                {
+                    double u = 0.0, g = 0.0;
+                    for (uint32_t k = 0; k < K; ++k)
+                    {
+                        double xv = rd(x, off4(x, b, c, m, k));
+                        u += xv * rd(wu, off4(wu, 0, 0, n, k));
+                        g += xv * rd(wg, off4(wg, 0, 0, n, k));
+                    }
+                    float uf = (float)u, gf = (float)g;
+                    wr(out, off4(out, b, c, m, n), uf * gf / (1.0f + expf(-gf)));
+                }
+    return 0;
+}

@@ -1,0 +1,64 @@
+"""Test helpers: deterministic inputs, fp16 ulp comparisons, oracle views of library tensors."""
+import numpy as np
+
+
+def rand(shape, dtype, lo=-1.0, hi=1.0, seed=0):
+    r = np.random.default_rng(seed)
+    return r.uniform(lo, hi, size=shape).astype(dtype)
+
+
+def fp16_ulp(x):
+    """Spacing of fp16 numbers at |x| (for x in the normal range; 2^-24 below it)."""
+    a = np.abs(np.asarray(x, dtype=np.float32))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -14)))
+    return np.float32(2.0) ** (e - 10)
+
+
+def ulp_diff(got, want):
+    """|got - want| in units of fp16 ulps of `want` (fp16 arrays)."""
+    g = got.astype(np.float32)
+    w = want.astype(np.float32)
+    return np.abs(g - w) / fp16_ulp(w)
+
+
+def assert_fp16_close(got, want, max_ulp=1.0, frac_exact=None, what="", atol=0.0):
+    """Every element within max_ulp fp16 ulps plus `atol` (the fp32 arithmetic's absolute error, which near zero
+    exceeds an ulp of the result); optionally at least frac_exact of them bit-identical."""
+    got = np.asarray(got)
+    want = np.asarray(want)
+    assert got.shape == want.shape, (got.shape, want.shape)
+    w = want.astype(np.float32)
+    d = np.maximum(np.abs(got.astype(np.float32) - w) - np.asarray(atol, dtype=np.float32), 0) / fp16_ulp(w)
+    worst = float(d.max()) if d.size else 0.0
+    assert worst <= max_ulp, f"{what}: max diff {worst:.2f} ulp > {max_ulp} (at {np.unravel_index(d.argmax(), d.shape)})"
+    if frac_exact is not None and got.size:
+        same = float(np.mean(got.view(np.uint16) == want.view(np.uint16))) if got.dtype == np.float16 else 1.0
+        assert same >= frac_exact, f"{what}: only {same:.4f} bit-identical (< {frac_exact})"
+
+
+U32 = 2.0 ** -24
+
+
+def dot_atol(a, b, transposed=True, k_axis=-1):
+    """Bound on fp32 accumulation error of a matmul: 16 units of fp32 roundoff times sum_k |a_k||b_k|."""
+    a64 = np.abs(a.astype(np.float64))
+    b64 = np.abs(b.astype(np.float64))
+    bb = np.swapaxes(b64, -1, -2) if transposed else b64
+    return (16 * U32 * np.matmul(a64, bb)).astype(np.float32)
+
+
+def mse(got, want):
+    return float(np.mean((got.astype(np.float64) - want.astype(np.float64)) ** 2))
+
+
+def bitrev5(x):
+    return int(f"{x:05b}"[::-1], 2)
+
+
+def argmax_tie_rule(row):
+    """The reference's arg max restated as a rule (src/shaders/vkllm_arg_max.comp:40-97): among the maximal
+    elements take the one whose lane (index mod 32) has the smallest 5-bit bit-reversal, then the smallest index."""
+    row = np.asarray(row, dtype=np.float32)
+    m = row.max()
+    cand = np.nonzero(row == m)[0]
+    return int(min(cand, key=lambda i: (bitrev5(int(i) % 32), int(i))))

@@ -1,0 +1,146 @@
+"""The LLaMA-2 token loop on the GPU through the C API (tests/vkllm_test_infer_gguf.c:173-272), against the oracle.
+
+Workload: the tiny LLaMA-2 (dim 288, 6 layers, 6 heads of 48, FFN 768, vocab 32000, ctx 256) from the seeded
+random-init GGUF, a 16-token prompt from seed 1, 64 greedy steps. Bar: identical greedy ids, logits within 2e-2.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+N_STEPS = 64
+LOGIT_TOL = 2e-2
+
+
+@pytest.fixture(scope="module")
+def reference_run(oracle, tiny_gguf):
+    m = oracle.Model(tiny_gguf)
+    prompt = oracle.prompt_tokens(1, 16, m.cfg.vocab)
+    ids, logits = m.token_loop(prompt, N_STEPS, want_logits=True)
+    m.close()
+    return prompt, ids, logits
+
+
+def _run(ctx, vk, path, prompt, mode, replay=True):
+    ctx.set_exec_mode(mode)
+    ctx.set_graph_replay(replay)
+    model = vk.Model(ctx, path=path)
+    try:
+        if mode == vk.EXEC_FUSED:
+            return model.token_loop(prompt, N_STEPS, want_logits=True)
+        ids, _ = model.token_loop(prompt, N_STEPS)
+        return ids, None
+    finally:
+        model.close()
+        ctx.set_exec_mode(vk.EXEC_FUSED)
+        ctx.set_graph_replay(True)
+
+
+def test_token_loop_fused_matches_oracle(ctx, vk, tiny_gguf, reference_run):
+    prompt, want_ids, want_logits = reference_run
+    ids, logits = _run(ctx, vk, tiny_gguf, prompt, vk.EXEC_FUSED)
+    err = np.max(np.abs(logits.astype(np.float32) - want_logits.astype(np.float32)), axis=1)
+    print(f"fused: max|dlogit| per step max {err.max():.3g} mean {err.mean():.3g}")
+    assert err.max() <= LOGIT_TOL
+    assert ids.tolist() == want_ids.tolist()
+
+
+def test_token_loop_nodes_matches_oracle(ctx, vk, tiny_gguf, reference_run):
+    """node-by-node execution of the same graphs through the VKLLM_OP_* kernels"""
+    prompt, want_ids, _ = reference_run
+    ids, _ = _run(ctx, vk, tiny_gguf, prompt, vk.EXEC_NODES)
+    assert ids.tolist() == want_ids.tolist()
+
+
+def test_graph_replay_matches_direct_launches(ctx, vk, tiny_gguf, reference_run):
+    prompt, _, _ = reference_run
+    a, la = _run(ctx, vk, tiny_gguf, prompt, vk.EXEC_FUSED, replay=True)
+    b, lb = _run(ctx, vk, tiny_gguf, prompt, vk.EXEC_FUSED, replay=False)
+    assert a.tolist() == b.tolist()
+    assert np.array_equal(la.view(np.uint16), lb.view(np.uint16))
+
+
+def test_prefill_at_kv_equal_head_dim(ctx, vk, oracle, tiny_gguf):
+    """A 48-token prompt makes kv == head_dim for the whole prefill: attn . V^T (src/core/vkllm_op_matmul.c:14-24)."""
+    m = oracle.Model(tiny_gguf)
+    prompt = oracle.prompt_tokens(2, 48, m.cfg.vocab)
+    want_ids, want_logits, _ = m.step(prompt, 0, want_logits=True)
+    m.close()
+    model = vk.Model(ctx, path=tiny_gguf)
+    try:
+        ids = model.step(prompt, 0)
+        logits = model.last_logits(48)
+    finally:
+        model.close()
+    assert np.max(np.abs(logits.astype(np.float32) - want_logits.astype(np.float32))) <= LOGIT_TOL
+    assert ids.tolist() == want_ids.tolist()
+
+
+def test_init_random_equals_gguf(ctx, vk, oracle, tiny_gguf):
+    """device-side random init (no file) gives the same weights as the GGUF written by the oracle"""
+    cfg = vk.llama_config(6, 288, 6, 768, vocab=32000, ctx=256)
+    a = vk.Model(ctx, path=tiny_gguf)
+    b = vk.Model(ctx, config=cfg, seed=0)
+    try:
+        for getter in (lambda m: m.weights.tok_embed_weights, lambda m: m.weights.output_weight,
+                       lambda m: m.weights.blocks.contents.data[0].contents.WQ,
+                       lambda m: m.weights.blocks.contents.data[5].contents.WD,
+                       lambda m: m.weights.blocks.contents.data[3].contents.WG,
+                       lambda m: m.weights.blocks.contents.data[3].contents.ffn_norm_weight):
+            ta, tb = getter(a.m), getter(b.m)
+            n = int(np.prod(list(ta.contents.shapes))) * (4 if ta.contents.dtype == vk.F32 else 2)
+            da, db = ctx.download_raw(ta, n), ctx.download_raw(tb, n)
+            assert np.array_equal(da, db)
+        prompt = oracle.prompt_tokens(1, 16, 32000)
+        assert a.step(prompt, 0).tolist() == b.step(prompt, 0).tolist()
+    finally:
+        a.close()
+        b.close()
+
+
+def test_graph_structure_matches_reference(ctx, vk, tiny_gguf):
+    """build_graph creates the reference's nodes: 23*L + 5 of them, names and ops in order
+    (src/models/vkllm_models_llama2.c:488-602, src/models/vkllm_llama2_layers.c:98-340)."""
+    import ctypes
+
+    L = vk.lib()
+    model = vk.Model(ctx, path=tiny_gguf)
+    try:
+        inp = ctx.tensor([1, 1, 1, 3], vk.U32, "input_toks", mapped=True)
+        g = ctypes.POINTER(vk.Graph)()
+        vk.check("graph_new", L.vkllm_graph_new(ctx.vp, ctypes.byref(g)))
+        vk.check("build", L.vkllm_models_llama2_build_graph(ctx.vp, ctypes.byref(model.m), inp, g, 5))
+        nodes = g.contents.nodes.contents
+        names = [nodes.data[i].contents.name.decode() for i in range(nodes.used_n)]
+        ops = [nodes.data[i].contents.op for i in range(nodes.used_n)]
+        assert len(names) == 23 * 6 + 5
+        assert names[:4] == ["input_toks", "embedded", "block.0.attn.norm", "block.0.attn.Q"]
+        blk = names[2:25]
+        assert blk == ["block.0.attn.norm", "block.0.attn.Q", "block.0.attn.K", "block.0.attn.V",
+                       "block.0.attn.Q_ref", "block.0.attn.K_ref", "block.0.attn.V_ref", "block.0.attn.RQ",
+                       "block.0.attn.RK", "block.0.attn.scores", "block.0.attn.attn_weights", "block.0.attn",
+                       "block.0.attn_ref", "block.0.attn.concated_heads", "block.0.attn.concated_heads_ref",
+                       "block.0.attn.final_output", "block.0.attn.final_output_add", "block.0.ffn.norm",
+                       "block.0.ffn.up", "block.0.ffn.gate", "block.0.ffn.mul", "block.0.ffn.down",
+                       "block.0.ffn.add"]
+        assert names[-3:] == ["output_norm", "logits", "output"]
+        assert ops[-1] == vk.OP_ARG_MAX and ops[-2] == vk.OP_MATMUL
+        out = g.contents.output_node.contents
+        assert list(out.shapes) == [1, 1, 3, 1] and out.dtype == vk.U32 and out.data.mapped
+        scores = nodes.data[11].contents
+        assert list(scores.shapes) == [1, 6, 3, 8]  # key_num = offset + S
+        vk.check("graph_free", L.vkllm_graph_free(ctx.vp, g))
+    finally:
+        model.close()
+
+
+def test_tokenizer(ctx, vk, tiny_gguf):
+    model = vk.Model(ctx, path=tiny_gguf)
+    try:
+        ids = model.tokenize("Q: What is the largest animal? A:")
+        texts = [model.meta.tokens.contents.data[i].text.decode() for i in ids[1:]]
+        assert ids[0] == model.meta.bos_token_id
+        assert "".join(texts).replace("▁", " ") == " Q: What is the largest animal? A:"
+        assert model.tokenize("") == []
+    finally:
+        model.close()

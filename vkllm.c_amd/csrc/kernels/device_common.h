@@ -1,0 +1,133 @@
+// Device-side helpers shared by the gfx950 kernels: fp16 casts (round-to-nearest-even), strided element access,
+// wave64 and workgroup reductions.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kernels.h"
+
+namespace vk
+{
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float h2f(uint16_t h)
+{
+    _Float16 v;
+    __builtin_memcpy(&v, &h, 2);
+    return (float)v;
+}
+
+__device__ __forceinline__ uint16_t f2h(float f)
+{
+    // The empty asm pins f as a rounded fp32 register value. Without it the backend folds fp16(a * b) into one
+    // v_fma_mixlo_f16 (exact product rounded once to fp16), which differs from rounding to fp32 and then to fp16.
+    asm("" : "+v"(f));
+    _Float16 v = (_Float16)f; // v_cvt_f16_f32, round-to-nearest-even
+    uint16_t h;
+    __builtin_memcpy(&h, &v, 2);
+    return h;
+}
+
+__device__ __forceinline__ size_t voff(const TView &t, uint32_t b, uint32_t c, uint32_t h, uint32_t w)
+{
+    return (size_t)b * t.s[0] + (size_t)c * t.s[1] + (size_t)h * t.s[2] + (size_t)w * t.s[3];
+}
+
+__device__ __forceinline__ float ldf(const TView &t, size_t off)
+{
+    switch (t.dt)
+    {
+    case DT_F32:
+        return ((const float *)t.p)[off];
+    case DT_F16:
+        return h2f(((const uint16_t *)t.p)[off]);
+    case DT_U32:
+        return (float)((const uint32_t *)t.p)[off];
+    default:
+        return (float)((const int8_t *)t.p)[off];
+    }
+}
+
+__device__ __forceinline__ void stf(const TView &t, size_t off, float v)
+{
+    switch (t.dt)
+    {
+    case DT_F32:
+        ((float *)t.p)[off] = v;
+        break;
+    case DT_F16:
+        ((uint16_t *)t.p)[off] = f2h(v);
+        break;
+    case DT_U32:
+        ((uint32_t *)t.p)[off] = (uint32_t)v;
+        break;
+    default:
+        ((int8_t *)t.p)[off] = (int8_t)v;
+        break;
+    }
+}
+
+// index -> (b, c, h, w) of shape n
+__device__ __forceinline__ void unflatten(uint64_t i, const uint32_t n[4], uint32_t &b, uint32_t &c, uint32_t &h,
+                                          uint32_t &w)
+{
+    w = (uint32_t)(i % n[3]);
+    i /= n[3];
+    h = (uint32_t)(i % n[2]);
+    i /= n[2];
+    c = (uint32_t)(i % n[1]);
+    b = (uint32_t)(i / n[1]);
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+        v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+// Sum over the workgroup; `red` holds one float per wave. All threads get the result.
+__device__ __forceinline__ float block_sum(float v, float *red)
+{
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave, nw = (blockDim.x + kWave - 1) / kWave;
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane == 0)
+        red[wid] = v;
+    __syncthreads();
+    float r = 0.f;
+    for (int i = 0; i < nw; ++i)
+        r += red[i];
+    return r;
+}
+
+__device__ __forceinline__ float block_max(float v, float *red)
+{
+    const int lane = threadIdx.x & (kWave - 1), wid = threadIdx.x / kWave, nw = (blockDim.x + kWave - 1) / kWave;
+    v = wave_max(v);
+    __syncthreads();
+    if (lane == 0)
+        red[wid] = v;
+    __syncthreads();
+    float r = red[0];
+    for (int i = 1; i < nw; ++i)
+        r = fmaxf(r, red[i]);
+    return r;
+}
+
+__device__ __forceinline__ float silu(float v)
+{
+    return v / (1.0f + expf(-v));
+}
+
+} // namespace vk

@@ -1,0 +1,116 @@
+// Launchers of the gfx950 kernels. Internal to libvkllm; every launcher enqueues on `stream` and returns the
+// launch status. Tensor views carry ELEMENT strides.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vk
+{
+
+enum DType : int32_t
+{
+    DT_F32 = 1,
+    DT_F16 = 2,
+    DT_I8 = 3,
+    DT_U32 = 4
+};
+
+struct TView
+{
+    void *p;
+    uint32_t n[4]; // shapes [N, C, H, W]
+    uint32_t s[4]; // element strides
+    int32_t dt;
+};
+
+// ---- generic operators (node-by-node execution and the op API) ----
+hipError_t launch_copy(hipStream_t st, const TView &in, const TView &out);
+hipError_t launch_bin(hipStream_t st, const TView &a, const TView &b, const TView &out, int op);
+hipError_t launch_embedding(hipStream_t st, const TView &idx, const TView &table, const TView &out, uint32_t unk);
+hipError_t launch_rmsnorm(hipStream_t st, const TView &x, const TView &w, const TView &out, float eps);
+// out = act(scale * a . b), b [N,K] when transposed_b else [K,N]; size-1 batch dims broadcast
+hipError_t launch_matmul(hipStream_t st, const TView &a, const TView &b, const TView &out, float scale, int act,
+                         bool transposed_b);
+// freqs_host[w] = base^(2w/D) for w < D/2 (D <= 2*kMaxRopeFreqs), passed by value in the kernel arguments
+constexpr int kMaxRopeFreqs = 256;
+hipError_t launch_rope(hipStream_t st, const TView &in, const TView &out, uint32_t offset, const float *freqs_host,
+                       bool neox);
+hipError_t launch_softmax(hipStream_t st, const TView &in, const TView &out, int seq_mask, uint32_t offsets);
+hipError_t launch_update_rows(hipStream_t st, const TView &src, const TView &cache, uint32_t offset_rows);
+hipError_t launch_arg_max(hipStream_t st, const TView &in, const TView &out);
+hipError_t launch_ffn_up_and_gate(hipStream_t st, const TView &x, const TView &wu, const TView &wg, const TView &out);
+
+// ---- fused LLaMA-2 token step ----
+// Device-resident step parameters, read by the kernels so a captured decode graph replays for any position.
+struct Step
+{
+    uint32_t offset; // position of the step's first token
+    uint32_t S;      // tokens in the step
+};
+
+// h[s] = embd[toks[s]] (ids >= V read row unk), s < S; D % 8 == 0
+hipError_t launch_embed_rows(hipStream_t st, const uint32_t *toks, uint32_t S, const uint16_t *embd, uint16_t *h,
+                             uint32_t V, uint32_t D, uint32_t unk);
+// y[s] = rmsnorm(x[s]) * w, s < S
+hipError_t launch_rmsnorm_rows(hipStream_t st, const uint16_t *x, const float *w, uint16_t *y, uint32_t S,
+                               uint32_t D, float eps);
+
+enum GemvEpi : int
+{
+    EPI_PLAIN = 0, // out[r] = fp16(acc_r)
+    EPI_RESID = 1, // out[r] = fp16(resid[r] + fp16(acc_r)), in place allowed
+    EPI_GATEUP = 2, // rows [0,F) up, [F,2F) gate: out[r] = fp16(fp16(up_r) * fp16(silu(gate_r)))
+    EPI_QKV = 3,   // rows [0,3D) of [Wq;Wk;Wv]: RoPE on q,k; q -> out, k/v -> caches at step->offset
+};
+
+struct GemvArgs
+{
+    const uint16_t *x;      // input vector [K] (the residual stream when norm_w is set)
+    const float *norm_w;    // RMSNorm weight: x is normalised in the prologue; nullptr: x used as is
+    float eps;
+    const uint16_t *w;      // weight rows [rows, K], K contiguous
+    uint32_t K;
+    uint32_t units;         // work units: PLAIN/RESID ceil(rows/2), GATEUP F, QKV 3D/2
+    uint32_t rows;          // weight rows
+    uint16_t *out;
+    const uint16_t *resid;  // EPI_RESID
+    // EPI_QKV
+    uint16_t *kc, *vc;      // layer caches [H, ctx, hd]
+    const Step *step;
+    const float *freqs;     // base^(2w/hd), w < hd/2
+    uint32_t D, hd, ctx;
+};
+hipError_t launch_gemv(hipStream_t st, int epi, const GemvArgs &a, int cu_count);
+
+// single-token attention over the cache for every head, one workgroup per head:
+// s_j = fp16(scale q.k_j), p = fp16(softmax(s)), out[h*hd + d] = fp16(sum_j p_j v_j[d]); kv = step->offset + 1.
+// When kv == hd the product is p . V^T (the reference's shape-based transposition rule).
+hipError_t launch_attn_decode(hipStream_t st, const uint16_t *q, const uint16_t *kc, const uint16_t *vc,
+                              uint16_t *out, const Step *step, uint32_t H, uint32_t hd, uint32_t ctx, float scale);
+// prefill: queries s < S at positions offset+s attend to positions <= offset+s
+hipError_t launch_attn_prefill(hipStream_t st, const uint16_t *q, const uint16_t *kc, const uint16_t *vc,
+                               uint16_t *out, uint32_t offset, uint32_t S, uint32_t H, uint32_t hd, uint32_t ctx,
+                               float scale);
+// qkv [S, 3D] -> RoPE'd q [S, D]; RoPE'd k and v into the caches at rows offset..offset+S-1
+hipError_t launch_rope_kv(hipStream_t st, const uint16_t *qkv, uint16_t *q, uint16_t *kc, uint16_t *vc,
+                          const float *freqs, uint32_t offset, uint32_t S, uint32_t D, uint32_t hd, uint32_t ctx);
+// act[s][n] = fp16(ug[s][n] * ug[s][F + n])
+hipError_t launch_swiglu(hipStream_t st, const uint16_t *ug, uint16_t *act, uint32_t S, uint32_t F);
+// ids[s] = arg_max(logits[s]) with the reference's tie rule, contiguous rows of V
+hipError_t launch_argmax_rows(hipStream_t st, const uint16_t *logits, uint32_t *ids, uint32_t S, uint32_t V);
+
+enum GemmEpi : int
+{
+    GEMM_PLAIN = 0,   // C = fp16(acc)
+    GEMM_SILU_HI = 1, // columns >= split: fp16(silu(acc)), others fp16(acc)
+    GEMM_RESID = 2,   // C = fp16(C + fp16(acc)) (C holds the residual)
+};
+// C[M, N] (row stride ldc) = A[M, K] . B[N, K]^T, fp16 operands, fp32 accumulation on MFMA. K % 8 == 0.
+hipError_t launch_gemm(hipStream_t st, int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, uint32_t M,
+                       uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, int cu_count);
+
+// ---- synthetic weights: dst[i] = fp16(normal(stream, i) * std), i < count ----
+hipError_t launch_random_f16(hipStream_t st, uint16_t *dst, uint64_t count, uint64_t stream_key, float std);
+hipError_t launch_fill_f32(hipStream_t st, float *dst, uint64_t count, float v);
+
+} // namespace vk

@@ -1,0 +1,528 @@
+// Stride-aware gfx950 kernels behind the VKLLM_OP_* operators (node-by-node execution and the op API).
+// They implement the operator semantics of the reference's shaders (src/shaders/*.comp) for any dtype mix and
+// any element strides; the LLaMA-2 token step itself runs on the fused kernels (fused_*.hip).
+#include <float.h>
+
+#include "device_common.h"
+#include "kernels.h"
+
+namespace vk
+{
+
+static inline uint32_t blocks_for(uint64_t n, uint32_t bs)
+{
+    return (uint32_t)((n + bs - 1) / bs);
+}
+
+static inline uint64_t numel(const TView &t)
+{
+    return (uint64_t)t.n[0] * t.n[1] * t.n[2] * t.n[3];
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// VKLLM_OP_COPY (src/shaders/vkllm_copy.comp:35-50) and VKLLM_OP_UPDATE_ROWS
+// (src/shaders/vkllm_update_rows.comp:21-46): raw element moves, bit-exact.
+template <typename T>
+__global__ void copy_kernel(TView in, TView out, uint64_t total, uint32_t row_offset)
+{
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (uint64_t)gridDim.x * blockDim.x)
+    {
+        uint32_t b, c, h, w;
+        unflatten(i, in.n, b, c, h, w);
+        if (h + row_offset >= out.n[2])
+            continue;
+        ((T *)out.p)[voff(out, b, c, h + row_offset, w)] = ((const T *)in.p)[voff(in, b, c, h, w)];
+    }
+}
+
+static hipError_t launch_move(hipStream_t st, const TView &in, const TView &out, uint32_t row_offset)
+{
+    uint64_t total = numel(in);
+    if (total == 0)
+        return hipSuccess;
+    uint32_t grid = blocks_for(total, 256);
+    grid = grid > 65536 ? 65536 : grid;
+    switch (in.dt)
+    {
+    case DT_F16:
+        copy_kernel<uint16_t><<<grid, 256, 0, st>>>(in, out, total, row_offset);
+        break;
+    case DT_I8:
+        copy_kernel<uint8_t><<<grid, 256, 0, st>>>(in, out, total, row_offset);
+        break;
+    default:
+        copy_kernel<uint32_t><<<grid, 256, 0, st>>>(in, out, total, row_offset);
+        break;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_copy(hipStream_t st, const TView &in, const TView &out)
+{
+    return launch_move(st, in, out, 0);
+}
+
+hipError_t launch_update_rows(hipStream_t st, const TView &src, const TView &cache, uint32_t offset_rows)
+{
+    return launch_move(st, src, cache, offset_rows);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// VKLLM_OP_BIN (src/shaders/vkllm_bin_op.comp:41-73): fp32 arithmetic, result rounded to the output dtype.
+__global__ void bin_kernel(TView a, TView b, TView out, int op, uint64_t total)
+{
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (uint64_t)gridDim.x * blockDim.x)
+    {
+        uint32_t n, c, h, w;
+        unflatten(i, out.n, n, c, h, w);
+        float x = ldf(a, voff(a, n, c, h, w)), y = ldf(b, voff(b, n, c, h, w));
+        float r = op == 0 ? x + y : op == 1 ? x - y : op == 2 ? x * y : x / y;
+        stf(out, voff(out, n, c, h, w), r);
+    }
+}
+
+hipError_t launch_bin(hipStream_t st, const TView &a, const TView &b, const TView &out, int op)
+{
+    uint64_t total = numel(out);
+    uint32_t grid = blocks_for(total, 256);
+    grid = grid > 65536 ? 65536 : grid;
+    bin_kernel<<<grid, 256, 0, st>>>(a, b, out, op, total);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// VKLLM_OP_EMBEDDING (src/shaders/vkllm_embedding.comp:138-167): one workgroup per index; index (0, c, h, w)
+// writes output row c*s0 + h*s1 + w*s2; ids >= rows read row `unk`.
+__global__ void embedding_kernel(TView idx, TView table, TView out, uint32_t unk)
+{
+    uint32_t b, c, h, w;
+    unflatten(blockIdx.x, idx.n, b, c, h, w);
+    uint32_t tok = ((const uint32_t *)idx.p)[voff(idx, b, c, h, w)];
+    const uint32_t rows = table.n[2], D = table.n[3];
+    if (tok >= rows)
+        tok = unk;
+    if (tok >= rows)
+        return;
+    size_t o = (size_t)c * out.s[0] + (size_t)h * out.s[1] + (size_t)w * out.s[2];
+    size_t p = (size_t)tok * table.s[2];
+    if (table.dt == DT_F16)
+        for (uint32_t i = threadIdx.x; i < D; i += blockDim.x)
+            ((uint16_t *)out.p)[o + (size_t)i * out.s[3]] = ((const uint16_t *)table.p)[p + (size_t)i * table.s[3]];
+    else
+        for (uint32_t i = threadIdx.x; i < D; i += blockDim.x)
+            ((uint32_t *)out.p)[o + (size_t)i * out.s[3]] = ((const uint32_t *)table.p)[p + (size_t)i * table.s[3]];
+}
+
+hipError_t launch_embedding(hipStream_t st, const TView &idx, const TView &table, const TView &out, uint32_t unk)
+{
+    uint64_t n = numel(idx);
+    if (n == 0)
+        return hipSuccess;
+    embedding_kernel<<<(uint32_t)n, 256, 0, st>>>(idx, table, out, unk);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// VKLLM_OP_RMSNORM (src/shaders/vkllm_rmsnorm.comp:31-82): alpha = 1/sqrt(sum(x^2)/W + eps), y = (x*w)*alpha.
+__global__ void rmsnorm_kernel(TView x, TView wt, TView out, float eps)
+{
+    __shared__ float red[16];
+    uint32_t b, c, h, w;
+    const uint32_t n3[4] = {x.n[0], x.n[1], x.n[2], 1};
+    unflatten(blockIdx.x, n3, b, c, h, w);
+    const uint32_t W = x.n[3];
+    size_t xr = voff(x, b, c, h, 0), orow = voff(out, b, c, h, 0);
+    float ss = 0.f;
+    for (uint32_t i = threadIdx.x; i < W; i += blockDim.x)
+    {
+        float v = ldf(x, xr + (size_t)i * x.s[3]);
+        ss += v * v;
+    }
+    ss = block_sum(ss, red);
+    float mean = ss / (float)W;
+    float alpha = 1.0f / sqrtf(mean + eps);
+    for (uint32_t i = threadIdx.x; i < W; i += blockDim.x)
+    {
+        float v0 = ldf(x, xr + (size_t)i * x.s[3]);
+        float v1 = ldf(wt, (size_t)i * wt.s[3]);
+        stf(out, orow + (size_t)i * out.s[3], (v0 * v1) * alpha);
+    }
+}
+
+hipError_t launch_rmsnorm(hipStream_t st, const TView &x, const TView &w, const TView &out, float eps)
+{
+    uint64_t rows = (uint64_t)x.n[0] * x.n[1] * x.n[2];
+    if (rows == 0)
+        return hipSuccess;
+    rmsnorm_kernel<<<(uint32_t)rows, 256, 0, st>>>(x, w, out, eps);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// VKLLM_OP_MATMUL and VKLLM_OP_FFN_UP_AND_GATE, generic path: 64x64 output tile per 256-thread workgroup, 4x4 per
+// thread, K staged through LDS in steps of 16, fp32 accumulation. Operands of any dtype and strides; size-1
+// batch/channel dims broadcast (src/core/vkllm_op_matmul.c:32-63). With DUAL, a second B operand gives
+// out = acc0 * silu(acc1) (src/shaders/vkllm_ffn_up_and_gate.comp:133-147).
+constexpr int GT = 64, GK = 16;
+
+template <bool DUAL>
+__global__ __launch_bounds__(256) void gemm_generic_kernel(TView a, TView b0, TView b1, TView out, float scale,
+                                                           int act, int transposed_b)
+{
+    __shared__ float As[GK][GT + 1];
+    __shared__ float Bs[DUAL ? 2 : 1][GK][GT + 1];
+    const uint32_t M = out.n[2], N = out.n[3], K = a.n[3];
+    const uint32_t bz = blockIdx.z / out.n[1], cz = blockIdx.z % out.n[1];
+    const uint32_t m0 = blockIdx.x * GT, n0 = blockIdx.y * GT;
+    const uint32_t ab = a.n[0] == 1 ? 0 : bz, ac = a.n[1] == 1 ? 0 : cz;
+    const uint32_t bb = b0.n[0] == 1 ? 0 : bz, bc = b0.n[1] == 1 ? 0 : cz;
+    const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+    float acc[2][4][4] = {};
+    for (uint32_t k0 = 0; k0 < K; k0 += GK)
+    {
+        for (int e = threadIdx.x; e < GT * GK; e += 256)
+        {
+            int r = e / GK, kk = e % GK;
+            uint32_t m = m0 + r, k = k0 + kk;
+            As[kk][r] = (m < M && k < K) ? ldf(a, voff(a, ab, ac, m, k)) : 0.f;
+            uint32_t n = n0 + r;
+            bool ok = n < N && k < K;
+#pragma unroll
+            for (int q = 0; q < (DUAL ? 2 : 1); ++q)
+            {
+                const TView &bv = q == 0 ? b0 : b1;
+                Bs[q][kk][r] = ok ? (transposed_b ? ldf(bv, voff(bv, bb, bc, n, k)) : ldf(bv, voff(bv, bb, bc, k, n)))
+                                  : 0.f;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < GK; ++kk)
+        {
+            float av[4], bv[2][4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                av[i] = As[kk][ty * 4 + i];
+#pragma unroll
+            for (int q = 0; q < (DUAL ? 2 : 1); ++q)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    bv[q][j] = Bs[q][kk][tx * 4 + j];
+#pragma unroll
+            for (int q = 0; q < (DUAL ? 2 : 1); ++q)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[q][i][j] = fmaf(av[i], bv[q][j], acc[q][i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+        {
+            uint32_t m = m0 + ty * 4 + i, n = n0 + tx * 4 + j;
+            if (m >= M || n >= N)
+                continue;
+            float v;
+            if (DUAL)
+            {
+                float g = acc[1][i][j];
+                v = acc[0][i][j] * g / (1.0f + expf(-g));
+            }
+            else
+            {
+                v = acc[0][i][j] * scale;
+                if (act == 1)
+                    v = silu(v);
+            }
+            stf(out, voff(out, bz, cz, m, n), v);
+        }
+}
+
+// M == 1 with B [N, K] (the reference's mat_mul_vec case, src/shaders/vkllm_mat_mul_vec.comp:115-171): one wave per
+// output element, lanes striding K.
+__global__ __launch_bounds__(256) void gemv_generic_kernel(TView a, TView b, TView out, float scale, int act)
+{
+    const uint32_t N = out.n[3];
+    const uint64_t total = (uint64_t)out.n[0] * out.n[1] * N;
+    const uint64_t wid = (uint64_t)blockIdx.x * (blockDim.x / kWave) + threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    if (wid >= total)
+        return;
+    const uint32_t n = (uint32_t)(wid % N), cz = (uint32_t)((wid / N) % out.n[1]), bz = (uint32_t)(wid / N / out.n[1]);
+    const uint32_t ab = a.n[0] == 1 ? 0 : bz, ac = a.n[1] == 1 ? 0 : cz;
+    const uint32_t bb = b.n[0] == 1 ? 0 : bz, bc = b.n[1] == 1 ? 0 : cz;
+    const uint32_t K = a.n[3];
+    float acc = 0.f;
+    for (uint32_t k = lane; k < K; k += kWave)
+        acc = fmaf(ldf(a, voff(a, ab, ac, 0, k)), ldf(b, voff(b, bb, bc, n, k)), acc);
+    acc = wave_sum(acc);
+    if (lane == 0)
+    {
+        float v = acc * scale;
+        if (act == 1)
+            v = silu(v);
+        stf(out, voff(out, bz, cz, 0, n), v);
+    }
+}
+
+hipError_t launch_matmul(hipStream_t st, const TView &a, const TView &b, const TView &out, float scale, int act,
+                         bool transposed_b)
+{
+    const uint32_t M = out.n[2], N = out.n[3];
+    const uint64_t batches = (uint64_t)out.n[0] * out.n[1];
+    if (M == 0 || N == 0 || batches == 0)
+        return hipSuccess;
+    if (M == 1 && transposed_b)
+    {
+        uint64_t waves = batches * N;
+        gemv_generic_kernel<<<blocks_for(waves, 4), 256, 0, st>>>(a, b, out, scale, act);
+        return hipGetLastError();
+    }
+    dim3 grid(blocks_for(M, GT), blocks_for(N, GT), (uint32_t)batches);
+    gemm_generic_kernel<false><<<grid, 256, 0, st>>>(a, b, b, out, scale, act, transposed_b ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_ffn_up_and_gate(hipStream_t st, const TView &x, const TView &wu, const TView &wg, const TView &out)
+{
+    const uint32_t M = out.n[2], N = out.n[3];
+    const uint64_t batches = (uint64_t)out.n[0] * out.n[1];
+    if (M == 0 || N == 0 || batches == 0)
+        return hipSuccess;
+    dim3 grid(blocks_for(M, GT), blocks_for(N, GT), (uint32_t)batches);
+    gemm_generic_kernel<true><<<grid, 256, 0, st>>>(x, wu, wg, out, 1.0f, 0, 1);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// VKLLM_OP_ROPE (src/shaders/vkllm_rope.comp:39-79): one thread per rotated pair.
+struct RopeFreqs
+{
+    float f[kMaxRopeFreqs];
+};
+
+__global__ void rope_kernel(TView in, TView out, uint32_t offset, RopeFreqs fr, int neox, uint64_t total)
+{
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (uint64_t)gridDim.x * blockDim.x)
+    {
+        const uint32_t half = in.n[3] / 2;
+        const uint32_t n4[4] = {in.n[0], in.n[1], in.n[2], half};
+        uint32_t b, c, h, w;
+        unflatten(i, n4, b, c, h, w);
+        size_t i0, i1, o0, o1;
+        if (neox)
+        {
+            i0 = voff(in, b, c, h, w);
+            i1 = i0 + (size_t)in.s[3] * half;
+            o0 = voff(out, b, c, h, w);
+            o1 = o0 + (size_t)out.s[3] * half;
+        }
+        else
+        {
+            i0 = voff(in, b, c, h, 2 * w);
+            i1 = i0 + in.s[3];
+            o0 = voff(out, b, c, h, 2 * w);
+            o1 = o0 + out.s[3];
+        }
+        float f = (float)(offset + h) / fr.f[w];
+        float fc = cosf(f), fs = sinf(f);
+        float v0 = ldf(in, i0), v1 = ldf(in, i1);
+        stf(out, o0, fc * v0 - fs * v1);
+        stf(out, o1, fs * v0 + fc * v1);
+    }
+}
+
+hipError_t launch_rope(hipStream_t st, const TView &in, const TView &out, uint32_t offset, const float *freqs_host,
+                       bool neox)
+{
+    RopeFreqs fr;
+    const uint32_t half = in.n[3] / 2;
+    if (half > (uint32_t)kMaxRopeFreqs)
+        return hipErrorInvalidValue;
+    for (uint32_t w = 0; w < half; ++w)
+        fr.f[w] = freqs_host[w];
+    uint64_t total = (uint64_t)in.n[0] * in.n[1] * in.n[2] * half;
+    if (total == 0)
+        return hipSuccess;
+    uint32_t grid = blocks_for(total, 256);
+    grid = grid > 65536 ? 65536 : grid;
+    rope_kernel<<<grid, 256, 0, st>>>(in, out, offset, fr, neox ? 1 : 0, total);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// VKLLM_OP_SOFTMAX (src/shaders/vkllm_softmax.comp:42-96): max over the whole row; with seq_mask, entries
+// i > h + offsets are excluded from the sum and written as 0.
+__global__ void softmax_kernel(TView in, TView out, int seq_mask, uint32_t offsets)
+{
+    __shared__ float red[16];
+    uint32_t b, c, h, w;
+    const uint32_t n3[4] = {out.n[0], out.n[1], out.n[2], 1};
+    unflatten(blockIdx.x, n3, b, c, h, w);
+    const uint32_t W = out.n[3];
+    size_t ir = voff(in, b, c, h, 0), orow = voff(out, b, c, h, 0);
+    float mx = -FLT_MAX;
+    for (uint32_t i = threadIdx.x; i < W; i += blockDim.x)
+        mx = fmaxf(mx, ldf(in, ir + (size_t)i * in.s[3]));
+    mx = block_max(mx, red);
+    const uint32_t lim = h + offsets;
+    float sum = 0.f;
+    for (uint32_t i = threadIdx.x; i < W; i += blockDim.x)
+        if (!(seq_mask > 0 && i > lim))
+            sum += expf(ldf(in, ir + (size_t)i * in.s[3]) - mx);
+    sum = block_sum(sum, red);
+    for (uint32_t i = threadIdx.x; i < W; i += blockDim.x)
+    {
+        float v = (seq_mask > 0 && i > lim) ? 0.f : expf(ldf(in, ir + (size_t)i * in.s[3]) - mx) / sum;
+        stf(out, orow + (size_t)i * out.s[3], v);
+    }
+}
+
+hipError_t launch_softmax(hipStream_t st, const TView &in, const TView &out, int seq_mask, uint32_t offsets)
+{
+    uint64_t rows = (uint64_t)out.n[0] * out.n[1] * out.n[2];
+    if (rows == 0)
+        return hipSuccess;
+    softmax_kernel<<<(uint32_t)rows, 256, 0, st>>>(in, out, seq_mask, offsets);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// VKLLM_OP_ARG_MAX (src/shaders/vkllm_arg_max.comp:40-97). The reference's 32 lanes each keep the first maximum of
+// the elements i == lane (mod 32); lanes then merge with a strict '>' tree over strides 16..1 where the lower lane
+// keeps ties. Here 256 threads split each lane's elements (thread t sees i == t (mod 256), all in lane t % 32), the
+// per-lane partials merge with "larger value, then smaller index", and the 32-lane tree runs exactly as written.
+__global__ __launch_bounds__(256) void arg_max_kernel(TView in, TView out)
+{
+    __shared__ float sv[256];
+    __shared__ uint32_t si[256];
+    __shared__ int sh[256];
+    uint32_t b, c, h, w;
+    const uint32_t n3[4] = {in.n[0], in.n[1], in.n[2], 1};
+    unflatten(blockIdx.x, n3, b, c, h, w);
+    const uint32_t W = in.n[3];
+    const size_t row = voff(in, b, c, h, 0);
+    const uint32_t t = threadIdx.x;
+    float bv = -FLT_MAX;
+    uint32_t bi = t % 32;
+    int have = 0;
+    if (t < 32)
+    {
+        have = 1;
+        if (t < W)
+            bv = ldf(in, row + (size_t)t * in.s[3]);
+    }
+    for (uint32_t i = (t < 32 ? t + 256 : t); i < W; i += 256)
+    {
+        float v = ldf(in, row + (size_t)i * in.s[3]);
+        if (!have || v > bv)
+        {
+            bv = v;
+            bi = i;
+            have = 1;
+        }
+    }
+    sv[t] = bv;
+    si[t] = bi;
+    sh[t] = have;
+    __syncthreads();
+    if (t < 32)
+    {
+        // merge the 8 threads of lane t (t, t+32, ..., t+224)
+        for (uint32_t k = t + 32; k < 256; k += 32)
+        {
+            if (!sh[k])
+                continue;
+            if (sv[k] > bv || (sv[k] == bv && si[k] < bi))
+            {
+                bv = sv[k];
+                bi = si[k];
+            }
+        }
+        sv[t] = bv;
+        si[t] = bi;
+    }
+    __syncthreads();
+    if (t == 0)
+    {
+        for (uint32_t s = 16; s > 0; s >>= 1)
+            for (uint32_t l = 0; l < s; ++l)
+                if (sv[l + s] > sv[l])
+                {
+                    sv[l] = sv[l + s];
+                    si[l] = si[l + s];
+                }
+        const uint32_t o3[4] = {out.n[0], out.n[1], out.n[2], 1};
+        (void)o3;
+        ((uint32_t *)out.p)[voff(out, b, c, h, 0)] = si[0];
+    }
+}
+
+hipError_t launch_arg_max(hipStream_t st, const TView &in, const TView &out)
+{
+    uint64_t rows = (uint64_t)in.n[0] * in.n[1] * in.n[2];
+    if (rows == 0)
+        return hipSuccess;
+    arg_max_kernel<<<(uint32_t)rows, 256, 0, st>>>(in, out);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// synthetic weights
+__device__ __forceinline__ uint64_t splitmix64(uint64_t stream, uint64_t n)
+{
+    uint64_t z = stream + (n + 1) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ void random_f16_kernel(uint16_t *dst, uint64_t count, uint64_t key, float std)
+{
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x)
+    {
+        int32_t sum = 0;
+#pragma unroll
+        for (int r = 0; r < 3; ++r)
+        {
+            uint64_t v = splitmix64(key, 3 * i + (uint64_t)r);
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                sum += (int32_t)((v >> (16 * k)) & 0xffffu);
+        }
+        float z = (float)(sum + 6 - 6 * 65536) / 65536.0f;
+        dst[i] = f2h(z * std);
+    }
+}
+
+hipError_t launch_random_f16(hipStream_t st, uint16_t *dst, uint64_t count, uint64_t stream_key, float std)
+{
+    if (count == 0)
+        return hipSuccess;
+    uint32_t grid = blocks_for(count, 256);
+    grid = grid > 8192 ? 8192 : grid;
+    random_f16_kernel<<<grid, 256, 0, st>>>(dst, count, stream_key, std);
+    return hipGetLastError();
+}
+
+__global__ void fill_f32_kernel(float *dst, uint64_t count, float v)
+{
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += (uint64_t)gridDim.x * blockDim.x)
+        dst[i] = v;
+}
+
+hipError_t launch_fill_f32(hipStream_t st, float *dst, uint64_t count, float v)
+{
+    if (count == 0)
+        return hipSuccess;
+    uint32_t grid = blocks_for(count, 256);
+    grid = grid > 8192 ? 8192 : grid;
+    fill_f32_kernel<<<grid, 256, 0, st>>>(dst, count, v);
+    return hipGetLastError();
+}
+
+} // namespace vk
