@@ -1,0 +1,250 @@
+#!/usr/bin/env python3
+"""Throughput of the vkllm LLaMA-2 token loop on one MI355X.
+
+Workload: LLaMA-2-7B-shaped decoder (dim 4096, 32 layers, 32 heads of 128, FFN 11008, vocab 32000), fp16
+weights generated on the device from seed 0 (weights N(0, 0.02), norm weights 1.0), a 128-token uniform-random
+prompt (seed 1) prefilled, then greedy decode at batch 1. Every token goes through the library's C API exactly
+as the reference's driver loop does (tests/vkllm_test_infer_gguf.c:183-270): tensor_new(input, mapped) ->
+graph_new -> models_llama2_build_graph -> graph_init -> upload -> graph_run -> graph_post_run ->
+tensor_invalid_cache -> read the arg-max id -> graph_free.
+
+Printed (one JSON line on stdout):
+  value        decode tokens/s over the timed steps (host loop included, inputs resident in HBM)
+  roofline     the dominant decode kernel (the fused RMSNorm + gate/up GEMV + SwiGLU): algorithmic bytes per
+               launch / its average duration, from one hipEvent pair on the library's stream around 128
+               back-to-back launches over the 32 layers' weights (the per-launch event pairs of the "kernels"
+               table include each launch's dispatch latency)
+  cpu_baseline the C oracle (scalar, double accumulation) timing a decode step of a 2-layer slice of the same
+               shape, scaled to 32 layers by multiply-accumulate count
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(HERE, "vkllm.c_amd"))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+
+SHAPE = dict(n_layer=32, dim=4096, n_head=32, ffn=11008, vocab=32000)
+PROMPT_LEN = 128
+MODEL_SEED, PROMPT_SEED = 0, 1
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def decode_bytes(shape, kv):
+    """Algorithmic HBM bytes of each fused decode kernel for one token at `kv` cached positions (fp16 weights
+    and activations, fp32 norm weights). Each weight is read once; activations and cache rows as written."""
+    D, F, V, L = shape["dim"], shape["ffn"], shape["vocab"], shape["n_layer"]
+    return {
+        "fused_embed": D * 2 * 2,
+        "fused_qkv_rope": 3 * D * D * 2 + D * 2 + D * 4 + D * 2 + 2 * D * 2,
+        "fused_attn_scores": 2 * kv * D * 2 + D * 2 + D * 2,
+        "fused_o_resid": D * D * 2 + D * 2 + 2 * D * 2,
+        "fused_gateup": 2 * F * D * 2 + D * 2 + D * 4 + F * 2,
+        "fused_down_resid": D * F * 2 + F * 2 + 2 * D * 2,
+        "fused_logits": V * D * 2 + D * 2 + D * 4 + V * 2,
+        "fused_argmax": V * 2 + 4,
+        "_layers": L,
+    }
+
+
+def read_traffic(kernel):
+    """HBM bytes per launch of `kernel` measured with rocprofv3 FETCH_SIZE/WRITE_SIZE, from the committed
+    summary profiles/<kernel>_7b_pmc.txt (line 'traffic_bytes_per_launch: N'); None when absent."""
+    path = os.path.join(HERE, "profiles", f"{kernel}_7b_pmc.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def copy_calibration(ctx, vk, mib):
+    """Runs the library's COPY op (contiguous fp16, `mib` MiB read and written) 4 times: a kernel of known HBM
+    traffic against which rocprofv3's FETCH_SIZE / WRITE_SIZE counters are scaled."""
+    import numpy as np
+
+    n = mib * (1 << 20) // 2
+    src = ctx.tensor_from(np.zeros(n, dtype=np.float16).reshape(1, 1, 1, n), name="calib_src")
+    dst = ctx.tensor([1, 1, 1, n], vk.F16, "calib_dst", vk.OP_COPY, [src])
+    for _ in range(4):
+        vk.check("copy", ctx.run_op("copy", dst))
+    ctx.free(dst)
+    ctx.free(src)
+    log(f"copy calibration: 4 copies of {mib} MiB")
+
+
+def cpu_baseline(seconds):
+    """Decode tokens/s of the C oracle on one host core. The sample is decode steps of a 2-layer model of the
+    same widths (dim 4096, FFN 11008, vocab 32000) from an empty cache, timed until `seconds` have passed,
+    scaled to 32 layers by multiply-accumulate count (matmuls are > 99% of the oracle's work)."""
+    sys.path.insert(0, os.path.join(HERE, "oracle"))
+    import oracle_ffi as oracle
+
+    D, F, V = SHAPE["dim"], SHAPE["ffn"], SHAPE["vocab"]
+    cfg = oracle.make_cfg(2, D, SHAPE["n_head"], F, vocab=V, ctx=64)
+    m = oracle.Model(cfg=cfg, seed=MODEL_SEED)
+    try:
+        tok = [int(oracle.prompt_tokens(PROMPT_SEED, 1, V)[0])]
+        n, t0 = 0, time.perf_counter()
+        while True:
+            ids, _, _ = m.step(tok, n)
+            tok = [int(ids[-1])]
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= seconds or n >= 60:
+                break
+    finally:
+        m.close()
+    mac_layer = 4 * D * D + 3 * D * F
+    scale = (SHAPE["n_layer"] * mac_layer + V * D) / (2 * mac_layer + V * D)
+    per_token = el / n * scale
+    return {
+        "value": round(1.0 / per_token, 5),
+        "unit": "tok/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"{n} decode steps of a 2-layer dim-4096/FFN-11008/vocab-32000 slice in {el:.1f} s on one core, "
+                  f"x{scale:.2f} by MAC count to 32 layers",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256, help="timed decode steps")
+    ap.add_argument("--warmup", type=int, default=8, help="untimed decode steps before the timed ones")
+    ap.add_argument("--prefill-reps", type=int, default=4, help="timed 128-token prefills")
+    ap.add_argument("--timing-steps", type=int, default=32, help="decode steps of the per-kernel timing pass")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample length (0: skip)")
+    ap.add_argument("--ctx", type=int, default=4096, help="KV cache positions")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="first run the COPY op on MIB MiB (reference kernel for rocprofv3 byte counters)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py runs on one GPU: the token loop of this library is single-device (asked for "
+              f"--gpus {args.gpus}, WORLD_SIZE {world})", file=sys.stderr)
+        sys.exit(2)
+    need = PROMPT_LEN + args.warmup + args.steps + args.timing_steps + 1
+    if need > args.ctx:
+        sys.exit(f"--ctx {args.ctx} is smaller than the {need} positions the run uses")
+
+    os.environ.setdefault("VKLLM_QUIET", "1")
+    import pyvkllm as vk
+
+    ctx = vk.Ctx(0)
+    if args.copy_calibration > 0:
+        copy_calibration(ctx, vk, args.copy_calibration)
+    log(f"device {ctx.arch()}; generating the 7B-shaped model on the device")
+    cfg = vk.llama_config(SHAPE["n_layer"], SHAPE["dim"], SHAPE["n_head"], SHAPE["ffn"], SHAPE["vocab"], args.ctx)
+    model = vk.Model(ctx, config=cfg, seed=MODEL_SEED)
+    prompt = vk.prompt_tokens(PROMPT_SEED, PROMPT_LEN, SHAPE["vocab"])
+
+    # prefill: one untimed, then timed repetitions of the same 128-token step at offset 0
+    model.step(prompt, 0)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.prefill_reps):
+        ids = model.step(prompt, 0)
+    ctx.sync()
+    prefill_s = (time.perf_counter() - t0) / args.prefill_reps
+    log(f"prefill {PROMPT_LEN} tokens: {prefill_s * 1e3:.2f} ms")
+
+    # decode
+    tok, pos = int(ids[-1]), PROMPT_LEN
+    for _ in range(args.warmup):
+        tok = int(model.step([tok], pos)[-1])
+        pos += 1
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        tok = int(model.step([tok], pos)[-1])
+        pos += 1
+    ctx.sync()
+    decode_s = time.perf_counter() - t0
+    tps = args.steps / decode_s
+    log(f"decode: {args.steps} steps in {decode_s:.3f} s = {tps:.1f} tok/s")
+
+    # per-kernel timing pass: direct launches, one hipEvent pair per launch on the library's stream
+    ctx.set_timing(True)
+    ctx.reset_kernel_stats()
+    kv_begin = pos
+    for _ in range(args.timing_steps):
+        tok = int(model.step([tok], pos)[-1])
+        pos += 1
+    ctx.sync()
+    stats = ctx.kernel_stats()
+    ctx.set_timing(False)
+    kv_mid = (kv_begin + pos) // 2 + 1
+    nbytes = decode_bytes(SHAPE, kv_mid)
+    kernels = {}
+    step_kernel_ns = 0.0
+    for name, (n, ns) in sorted(stats.items(), key=lambda kv: -kv[1][1]):
+        avg_ns = ns / n
+        step_kernel_ns += ns / args.timing_steps
+        row = {"launches": n, "avg_us": round(avg_ns / 1e3, 3)}
+        if name in nbytes:
+            row["GBps"] = round(nbytes[name] / avg_ns, 1)
+        kernels[name] = row
+        log(f"  {name:20s} {n:6d} launches  avg {avg_ns / 1e3:9.2f} us  {row.get('GBps', '')}")
+    # the dominant kernel: back-to-back launches over the 32 layers' weights between one hipEvent pair
+    dom = "fused_gateup"
+    dom_avg_ns = model.time_kernel(dom, 4 * SHAPE["n_layer"])
+    log(f"  {dom}: {dom_avg_ns / 1e3:.2f} us per back-to-back launch")
+    achieved = nbytes[dom] / dom_avg_ns  # GB/s
+    step_bytes = sum(v for k, v in nbytes.items() if k in ("fused_qkv_rope", "fused_attn_scores", "fused_o_resid",
+                                                           "fused_gateup", "fused_down_resid")) * SHAPE["n_layer"]
+    step_bytes += nbytes["fused_embed"] + nbytes["fused_logits"] + nbytes["fused_argmax"]
+    traffic = read_traffic(dom)
+
+    result = {
+        "metric": "decode tok/s + % HBM roofline, LLaMA-2-7B-shape fp16 bs=1; prefill tok/s",
+        "value": round(tps, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(decode_s / args.steps * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 storage, f32 accumulate",
+        "data": "synthetic: device-generated random-init weights (seed 0), uniform-random prompt ids (seed 1)",
+        "config": {"workload": "LLaMA-2-7B-shaped decoder (dim 4096, 32 layers, 32 heads, FFN 11008, vocab 32000), "
+                               "128-token prompt prefill then greedy decode at batch 1",
+                   "prompt": PROMPT_LEN, "decode_positions": [PROMPT_LEN + args.warmup,
+                                                              PROMPT_LEN + args.warmup + args.steps],
+                   "kv_cache_positions": args.ctx},
+        "prefill_tok_s": round(PROMPT_LEN / prefill_s, 1),
+        "prefill_ms": round(prefill_s * 1e3, 3),
+        "decode_hbm_roofline_frac": round(step_bytes / (decode_s / args.steps) / 1e9 / HBM_PEAK_GBS, 4),
+        "decode_bytes_per_token": step_bytes,
+        "kernel_ms_per_step": round(step_kernel_ns / 1e6, 4),
+        "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes": nbytes[dom], "avg_us": round(dom_avg_ns / 1e3, 3)},
+        "kernels": kernels,
+    }
+    model.close()
+    ctx.close()
+    if args.cpu_seconds > 0:
+        log("cpu baseline (oracle, one core)")
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

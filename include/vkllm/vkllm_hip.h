@@ -26,6 +26,23 @@ extern vkllm_err_t vkllm_hip_set_graph_replay(struct vkllm_context *context, int
 /* per-launch hipEvent timing feeding vkllm_pipeline_query_exec_time and context->stats (also VKLLM_TIMING=1) */
 extern vkllm_err_t vkllm_hip_set_timing(struct vkllm_context *context, int enable);
 
+/* Number of kernel families (pipelines) of the library. */
+extern int vkllm_hip_kernel_family_count(void);
+/* Timing counters of kernel family `index` (0 <= index < vkllm_hip_kernel_family_count(), else VKLLM_ERR_ARGS):
+ * its name, the number of timed launches and their summed duration in nanoseconds. Waits for pending launches. */
+extern vkllm_err_t vkllm_hip_kernel_stats(struct vkllm_context *context, int index, const char **name,
+                                          uint64_t *launches, uint64_t *total_ns);
+/* Zeroes every kernel family's timing counters. */
+extern vkllm_err_t vkllm_hip_reset_kernel_stats(struct vkllm_context *context);
+
+/* Launches the decode-step kernel `family` `reps` times back to back, cycling over the layers' weights, between
+ * one hipEvent pair on the context's stream, and returns the elapsed nanoseconds: the kernel's duration without
+ * the per-launch dispatch latency that a per-launch event pair adds. The kernel must leave the model's state
+ * unchanged when repeated; supported: "fused_gateup" (RMSNorm + [Wu;Wg] GEMV + SwiGLU into a scratch buffer).
+ * Needs a preceding single-token step of `model`. */
+extern vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *context, struct vkllm_models_llama2 *model,
+                                               const char *family, uint32_t reps, uint64_t *total_ns);
+
 /* Model configuration for vkllm_models_llama2_init_random. */
 struct vkllm_llama2_config
 {

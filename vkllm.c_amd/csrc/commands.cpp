@@ -130,6 +130,7 @@ extern "C" vkllm_err_t vkllm_commands_wait_exec(struct vkllm_context *context, s
         HIP_TRY(hipMemcpyAsync(t->data.host, t->data.dev, t->bytes, hipMemcpyDeviceToHost, st));
     }
     HIP_TRY(hipStreamSynchronize(st));
+    HIP_TRY(timing_flush(context));
     commands->written_mapped->used_n = 0;
     vkllm_err_t rc = VKLLM_ERR_OK;
     for (size_t i = 0; i < commands->defer_tasks->used_n; ++i)

@@ -210,27 +210,72 @@ vkllm_pipeline *pipeline_of(vkllm_context *ctx, KernelId id)
     return &ctx->pipelines->entries[id];
 }
 
+static hipEvent_t pooled_event(vkllm_gpu_device *dev)
+{
+    if (!dev->event_pool.empty())
+    {
+        hipEvent_t e = dev->event_pool.back();
+        dev->event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess)
+        return nullptr;
+    return e;
+}
+
 void timing_begin(vkllm_context *ctx, vkllm_pipeline *p)
 {
-    if (!ctx->device->timing)
+    vkllm_gpu_device *dev = ctx->device;
+    if (!dev->timing)
         return;
-    if (!p->ev_begin)
-    {
-        hipEvent_t a, b;
-        if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess)
-            return;
-        p->ev_begin = a;
-        p->ev_end = b;
-    }
-    (void)hipEventRecord((hipEvent_t)p->ev_begin, ctx->device->stream);
+    hipEvent_t b = pooled_event(dev);
+    p->ev_begin = b;
+    if (b)
+        (void)hipEventRecord(b, dev->stream);
 }
 
 void timing_end(vkllm_context *ctx, vkllm_pipeline *p)
 {
-    if (!ctx->device->timing || !p->ev_end)
+    vkllm_gpu_device *dev = ctx->device;
+    if (!dev->timing || !p->ev_begin)
         return;
-    (void)hipEventRecord((hipEvent_t)p->ev_end, ctx->device->stream);
+    hipEvent_t e = pooled_event(dev);
+    if (!e)
+        return;
+    (void)hipEventRecord(e, dev->stream);
+    dev->timing_pending.push_back({p, (hipEvent_t)p->ev_begin, e});
+    p->ev_begin = nullptr;
     p->pending = 1;
+    // bound the number of events in flight; the flush waits for the oldest launches only
+    if (dev->timing_pending.size() >= 4096)
+        (void)timing_flush(ctx);
+}
+
+hipError_t timing_flush(vkllm_context *ctx)
+{
+    vkllm_gpu_device *dev = ctx->device;
+    hipError_t rc = hipSuccess;
+    for (auto &r : dev->timing_pending)
+    {
+        float ms = 0.f;
+        hipError_t e = hipEventSynchronize(r.end);
+        if (e == hipSuccess)
+            e = hipEventElapsedTime(&ms, r.begin, r.end);
+        if (e == hipSuccess)
+        {
+            r.pipeline->last_ns = (uint64_t)((double)ms * 1e6);
+            r.pipeline->total_ns += r.pipeline->last_ns;
+            r.pipeline->launches += 1;
+        }
+        else if (rc == hipSuccess)
+            rc = e;
+        r.pipeline->pending = 0;
+        dev->event_pool.push_back(r.begin);
+        dev->event_pool.push_back(r.end);
+    }
+    dev->timing_pending.clear();
+    return rc;
 }
 
 extern "C" vkllm_err_t vkllm_pipeline_query_exec_time(struct vkllm_context *context, struct vkllm_pipeline *pipeline,
@@ -238,17 +283,41 @@ extern "C" vkllm_err_t vkllm_pipeline_query_exec_time(struct vkllm_context *cont
 {
     _CHECK_ARGS(context && pipeline && cost);
     _CHECK_ARGS(context->device->timing);
-    if (pipeline->pending)
-    {
-        HIP_TRY(hipEventSynchronize((hipEvent_t)pipeline->ev_end));
-        float ms = 0.f;
-        HIP_TRY(hipEventElapsedTime(&ms, (hipEvent_t)pipeline->ev_begin, (hipEvent_t)pipeline->ev_end));
-        pipeline->last_ns = (uint64_t)((double)ms * 1e6);
-        pipeline->total_ns += pipeline->last_ns;
-        pipeline->launches += 1;
-        pipeline->pending = 0;
-    }
+    HIP_TRY(timing_flush(context));
     *cost = pipeline->last_ns;
+    return VKLLM_ERR_OK;
+}
+
+extern "C" int vkllm_hip_kernel_family_count(void)
+{
+    return KID_COUNT;
+}
+
+extern "C" vkllm_err_t vkllm_hip_kernel_stats(struct vkllm_context *context, int index, const char **name,
+                                              uint64_t *launches, uint64_t *total_ns)
+{
+    _CHECK_ARGS(context && index >= 0 && index < KID_COUNT);
+    HIP_TRY(timing_flush(context));
+    const vkllm_pipeline &p = context->pipelines->entries[index];
+    if (name)
+        *name = p.name;
+    if (launches)
+        *launches = p.launches;
+    if (total_ns)
+        *total_ns = p.total_ns;
+    return VKLLM_ERR_OK;
+}
+
+extern "C" vkllm_err_t vkllm_hip_reset_kernel_stats(struct vkllm_context *context)
+{
+    _CHECK_ARGS(context);
+    HIP_TRY(timing_flush(context));
+    for (int i = 0; i < KID_COUNT; ++i)
+    {
+        context->pipelines->entries[i].last_ns = 0;
+        context->pipelines->entries[i].total_ns = 0;
+        context->pipelines->entries[i].launches = 0;
+    }
     return VKLLM_ERR_OK;
 }
 
@@ -323,13 +392,9 @@ extern "C" void vkllm_context_free(struct vkllm_context *ctx)
         if (ctx->device->stream)
             (void)hipStreamSynchronize(ctx->device->stream);
         if (ctx->pipelines)
-            for (int i = 0; i < KID_COUNT; ++i)
-            {
-                if (ctx->pipelines->entries[i].ev_begin)
-                    (void)hipEventDestroy((hipEvent_t)ctx->pipelines->entries[i].ev_begin);
-                if (ctx->pipelines->entries[i].ev_end)
-                    (void)hipEventDestroy((hipEvent_t)ctx->pipelines->entries[i].ev_end);
-            }
+            (void)timing_flush(ctx);
+        for (hipEvent_t e : ctx->device->event_pool)
+            (void)hipEventDestroy(e);
         pool_release_all(ctx->device);
         if (ctx->device->stream)
             (void)hipStreamDestroy(ctx->device->stream);
@@ -374,6 +439,7 @@ extern "C" vkllm_err_t vkllm_hip_synchronize(struct vkllm_context *ctx)
 {
     _CHECK_ARGS(ctx);
     HIP_TRY(hipStreamSynchronize(ctx->device->stream));
+    HIP_TRY(timing_flush(ctx));
     return VKLLM_ERR_OK;
 }
 

@@ -144,6 +144,21 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
             return hip_fail(_e, #_call, __FILE__, __LINE__);                                                        \
     } while (0)
 
+// RMSNorm(h) -> [Wu;Wg] GEMV -> up * silu(gate) into act, for layer l of a decode step
+static vk::GemvArgs gateup_args(const ModelPriv *mp, uint32_t l)
+{
+    vk::GemvArgs gu{};
+    gu.x = mp->fs->h;
+    gu.norm_w = mp->layers[l].ffn_norm;
+    gu.eps = mp->eps;
+    gu.w = mp->layers[l].wug;
+    gu.K = mp->D;
+    gu.rows = 2 * mp->F;
+    gu.units = mp->F;
+    gu.out = mp->fs->act;
+    return gu;
+}
+
 // decode: S == 1, position from fs->step
 static vkllm_err_t enqueue_decode(vkllm_context *ctx, ModelPriv *mp)
 {
@@ -184,16 +199,7 @@ static vkllm_err_t enqueue_decode(vkllm_context *ctx, ModelPriv *mp)
         o.out = fs->h;
         o.resid = fs->h;
         KTRY(ctx, KID_F_O_RESID, vk::launch_gemv(st, vk::EPI_RESID, o, cu));
-        vk::GemvArgs gu{};
-        gu.x = fs->h;
-        gu.norm_w = ly.ffn_norm;
-        gu.eps = mp->eps;
-        gu.w = ly.wug;
-        gu.K = D;
-        gu.rows = 2 * F;
-        gu.units = F;
-        gu.out = fs->act;
-        KTRY(ctx, KID_F_GATEUP, vk::launch_gemv(st, vk::EPI_GATEUP, gu, cu));
+        KTRY(ctx, KID_F_GATEUP, vk::launch_gemv(st, vk::EPI_GATEUP, gateup_args(mp, l), cu));
         vk::GemvArgs dn{};
         dn.x = fs->act;
         dn.w = ly.wd;
@@ -337,5 +343,41 @@ extern "C" vkllm_err_t vkllm_hip_model_last_logits(struct vkllm_context *ctx, st
     HIP_TRY(hipMemcpyAsync(dst, mp->fs->logits, (size_t)rows * mp->V * 2, hipMemcpyDeviceToHost,
                            ctx->device->stream));
     HIP_TRY(hipStreamSynchronize(ctx->device->stream));
+    return VKLLM_ERR_OK;
+}
+
+extern "C" vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *ctx, struct vkllm_models_llama2 *model,
+                                                   const char *family, uint32_t reps, uint64_t *total_ns)
+{
+    _CHECK_ARGS(ctx && model && family && reps > 0 && total_ns);
+    ModelPriv *mp = model_priv(model);
+    _CHECK_ARGS(mp && mp->fs && mp->fs->cap_S >= 1 && mp->fs->h);
+    _CHECK_ARGS(strcmp(family, "fused_gateup") == 0);
+    hipStream_t st = ctx->device->stream;
+    const int cu = ctx->device->cu_count;
+    // one untimed launch so the first timed one does not pay for code loading
+    HIP_TRY(vk::launch_gemv(st, vk::EPI_GATEUP, gateup_args(mp, 0), cu));
+    hipEvent_t ev[2];
+    HIP_TRY(hipEventCreate(&ev[0]));
+    if (hipEventCreate(&ev[1]) != hipSuccess)
+    {
+        (void)hipEventDestroy(ev[0]);
+        return VKLLM_ERR_VULKAN;
+    }
+    hipError_t e = hipEventRecord(ev[0], st);
+    for (uint32_t r = 0; r < reps && e == hipSuccess; ++r)
+        e = vk::launch_gemv(st, vk::EPI_GATEUP, gateup_args(mp, (r + 1) % mp->L), cu);
+    if (e == hipSuccess)
+        e = hipEventRecord(ev[1], st);
+    if (e == hipSuccess)
+        e = hipEventSynchronize(ev[1]);
+    float ms = 0.f;
+    if (e == hipSuccess)
+        e = hipEventElapsedTime(&ms, ev[0], ev[1]);
+    (void)hipEventDestroy(ev[0]);
+    (void)hipEventDestroy(ev[1]);
+    if (e != hipSuccess)
+        return hip_fail(e, "vkllm_hip_model_time_kernel", __FILE__, __LINE__);
+    *total_ns = (uint64_t)((double)ms * 1e6);
     return VKLLM_ERR_OK;
 }

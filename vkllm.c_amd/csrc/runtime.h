@@ -76,6 +76,14 @@ struct vkllm_gpu_device
     int exec_mode = VKLLM_EXEC_FUSED;
     int graph_replay = 1;
     int timing = 0;
+    // timing mode: one event pair per launch, resolved into the pipelines' counters at synchronisation points
+    struct TimingRec
+    {
+        vkllm_pipeline *pipeline;
+        hipEvent_t begin, end;
+    };
+    std::vector<TimingRec> timing_pending;
+    std::vector<hipEvent_t> event_pool;
 };
 
 // ---- errors ----
@@ -110,6 +118,8 @@ vkllm_pipeline *pipeline_of(vkllm_context *ctx, KernelId id);
 template <typename F> hipError_t timed(vkllm_context *ctx, vkllm_pipeline *p, F &&fn);
 void timing_begin(vkllm_context *ctx, vkllm_pipeline *p);
 void timing_end(vkllm_context *ctx, vkllm_pipeline *p);
+// Waits for the recorded launches and adds their durations to their pipelines' last_ns/total_ns/launches.
+hipError_t timing_flush(vkllm_context *ctx);
 
 template <typename F> hipError_t timed(vkllm_context *ctx, vkllm_pipeline *p, F &&fn)
 {

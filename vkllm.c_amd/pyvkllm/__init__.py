@@ -204,6 +204,12 @@ def lib():
             "vkllm_hip_set_graph_replay": (E, [vp, E]),
             "vkllm_hip_set_timing": (E, [vp, E]),
             "vkllm_hip_synchronize": (E, [vp]),
+            "vkllm_hip_kernel_stats": (E, [vp, E, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_uint64),
+                                           ctypes.POINTER(ctypes.c_uint64)]),
+            "vkllm_hip_reset_kernel_stats": (E, [vp]),
+            "vkllm_hip_kernel_family_count": (E, []),
+            "vkllm_hip_model_time_kernel": (E, [vp, ctypes.POINTER(ModelStruct), ctypes.c_char_p, u32,
+                                                ctypes.POINTER(ctypes.c_uint64)]),
             "vkllm_hip_device_arch": (ctypes.c_char_p, [vp]),
             "vkllm_hip_model_last_logits": (E, [vp, ctypes.POINTER(ModelStruct), vp, u32]),
             "vkllm_hip_abi_layout": (E, [ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_uint64), E]),
@@ -323,6 +329,20 @@ class Ctx:
     def sync(self):
         check("vkllm_hip_synchronize", lib().vkllm_hip_synchronize(self.vp))
 
+    def kernel_stats(self):
+        """{kernel family name: (timed launches, summed nanoseconds)} for the families launched while timing."""
+        out = {}
+        name, n, ns = ctypes.c_char_p(), ctypes.c_uint64(), ctypes.c_uint64()
+        for i in range(lib().vkllm_hip_kernel_family_count()):
+            check("vkllm_hip_kernel_stats",
+                  lib().vkllm_hip_kernel_stats(self.vp, i, ctypes.byref(name), ctypes.byref(n), ctypes.byref(ns)))
+            if n.value:
+                out[name.value.decode()] = (n.value, ns.value)
+        return out
+
+    def reset_kernel_stats(self):
+        check("vkllm_hip_reset_kernel_stats", lib().vkllm_hip_reset_kernel_stats(self.vp))
+
     # ---- tensors ----
     def tensor(self, shapes, dtype, name="t", op=OP_NONE, srcs=(), params=None, mapped=False):
         """vkllm_tensor_new; params is a ctypes object or None."""
@@ -432,6 +452,13 @@ class Model:
         libc.free(ctypes.cast(ids, ctypes.c_void_p))
         return out
 
+    def time_kernel(self, family, reps):
+        """Average nanoseconds of `reps` back-to-back launches of a decode kernel (after a decode step)."""
+        ns = ctypes.c_uint64()
+        check("vkllm_hip_model_time_kernel", lib().vkllm_hip_model_time_kernel(
+            self.ctx.vp, ctypes.byref(self.m), family.encode(), reps, ctypes.byref(ns)))
+        return ns.value / reps
+
     def last_logits(self, rows):
         out = np.zeros((rows, self.meta.vocab_size), dtype=np.float16)
         check("vkllm_hip_model_last_logits",
@@ -480,6 +507,20 @@ class Model:
             out.append(int(ids[-1]))
             toks = np.array([out[-1]], dtype=np.uint32)
         return np.array(out, dtype=np.uint32), (np.stack(logits) if want_logits else None)
+
+
+def splitmix64(stream, n):
+    """Counter-based SplitMix64 word n of `stream`: the generator behind every synthetic input of this library."""
+    m = (1 << 64) - 1
+    z = (stream + (n + 1) * 0x9E3779B97F4A7C15) & m
+    z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & m
+    z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & m
+    return z ^ (z >> 31)
+
+
+def prompt_tokens(seed, n, vocab):
+    """Uniform-random prompt: token i = splitmix64(seed, i) mod vocab."""
+    return np.array([splitmix64(seed, i) % vocab for i in range(n)], dtype=np.uint32)
 
 
 def llama_config(n_layer, dim, n_head, ffn, vocab=32000, ctx=256, eps=1e-5, theta=10000.0, std=0.02):
