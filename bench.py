@@ -8,12 +8,16 @@ as the reference's driver loop does (tests/vkllm_test_infer_gguf.c:183-270): ten
 graph_new -> models_llama2_build_graph -> graph_init -> upload -> graph_run -> graph_post_run ->
 tensor_invalid_cache -> read the arg-max id -> graph_free.
 
+The loop runs in C (vkllm_hip_token_loop, the same API calls), so no interpreter sits between tokens.
+
 Printed (one JSON line on stdout):
-  value        decode tokens/s over the timed steps (host loop included, inputs resident in HBM)
+  value        decode tokens/s over exactly `--steps` timed single-token steps of that loop (host work included,
+               weights and KV cache resident in HBM)
+  graph_replay_tok_s  the same decode step as back-to-back replays of its captured hipGraph (device time only)
+  kernels      each decode kernel's average duration over back-to-back launches between one hipEvent pair on the
+               library's stream, and its algorithmic GB/s
   roofline     the dominant decode kernel (the fused RMSNorm + gate/up GEMV + SwiGLU): algorithmic bytes per
-               launch / its average duration, from one hipEvent pair on the library's stream around 128
-               back-to-back launches over the 32 layers' weights (the per-launch event pairs of the "kernels"
-               table include each launch's dispatch latency)
+               launch / its average duration over 128 back-to-back launches across the 32 layers' weights
   cpu_baseline the C oracle (scalar, double accumulation) timing a decode step of a 2-layer slice of the same
                shape, scaled to 32 layers by multiply-accumulate count
 """
@@ -23,6 +27,8 @@ import os
 import sys
 import time
 
+import numpy as np
+
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(HERE, "vkllm.c_amd"))
 
@@ -30,6 +36,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 
 SHAPE = dict(n_layer=32, dim=4096, n_head=32, ffn=11008, vocab=32000)
 PROMPT_LEN = 128
+ATTN_SMALL_MAX = 1024  # positions up to which the decode attention is one kernel (VKLLM_ATTN_SMALL_MAX)
 MODEL_SEED, PROMPT_SEED = 0, 1
 
 
@@ -45,6 +52,7 @@ def decode_bytes(shape, kv):
         "fused_embed": D * 2 * 2,
         "fused_qkv_rope": 3 * D * D * 2 + D * 2 + D * 4 + D * 2 + 2 * D * 2,
         "fused_attn_scores": 2 * kv * D * 2 + D * 2 + D * 2,
+        "fused_attn_small": 2 * kv * D * 2 + D * 2 + D * 2,
         "fused_o_resid": D * D * 2 + D * 2 + 2 * D * 2,
         "fused_gateup": 2 * F * D * 2 + D * 2 + D * 4 + F * 2,
         "fused_down_resid": D * F * 2 + F * 2 + 2 * D * 2,
@@ -124,7 +132,7 @@ def main():
     ap.add_argument("--steps", type=int, default=256, help="timed decode steps")
     ap.add_argument("--warmup", type=int, default=8, help="untimed decode steps before the timed ones")
     ap.add_argument("--prefill-reps", type=int, default=4, help="timed 128-token prefills")
-    ap.add_argument("--timing-steps", type=int, default=32, help="decode steps of the per-kernel timing pass")
+    ap.add_argument("--timing-steps", type=int, default=32, help="graph replays timed for the device-only rate")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample length (0: skip)")
     ap.add_argument("--ctx", type=int, default=4096, help="KV cache positions")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -151,61 +159,62 @@ def main():
     model = vk.Model(ctx, config=cfg, seed=MODEL_SEED)
     prompt = vk.prompt_tokens(PROMPT_SEED, PROMPT_LEN, SHAPE["vocab"])
 
-    # prefill: one untimed, then timed repetitions of the same 128-token step at offset 0
-    model.step(prompt, 0)
-    ctx.sync()
-    t0 = time.perf_counter()
+    # prefill: one untimed, then timed repetitions of the same 128-token step at offset 0, each through the
+    # C token loop (one step: tensor_new, graph_new, build_graph, init, upload, run, post_run, free)
+    model.loop(prompt, 1)
+    prefill_ns = []
     for _ in range(args.prefill_reps):
-        ids = model.step(prompt, 0)
-    ctx.sync()
-    prefill_s = (time.perf_counter() - t0) / args.prefill_reps
-    log(f"prefill {PROMPT_LEN} tokens: {prefill_s * 1e3:.2f} ms")
+        _, sns, _ = model.loop(prompt, 1)
+        prefill_ns.append(int(sns[0]))
+    prefill_s = float(np.median(prefill_ns)) / 1e9
+    log(f"prefill {PROMPT_LEN} tokens: {prefill_s * 1e3:.2f} ms (median of {args.prefill_reps})")
 
-    # decode
-    tok, pos = int(ids[-1]), PROMPT_LEN
-    for _ in range(args.warmup):
-        tok = int(model.step([tok], pos)[-1])
-        pos += 1
+    # decode: prefill + warmup steps untimed, then exactly `steps` single-token steps in one C loop
+    ids, _, _ = model.loop(prompt, 1 + args.warmup)
+    pos = PROMPT_LEN + args.warmup
     ctx.sync()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        tok = int(model.step([tok], pos)[-1])
-        pos += 1
+    ids, step_ns, phase_ns = model.loop([int(ids[-1])], args.steps, offset=pos)
     ctx.sync()
     decode_s = time.perf_counter() - t0
+    pos += args.steps
     tps = args.steps / decode_s
-    log(f"decode: {args.steps} steps in {decode_s:.3f} s = {tps:.1f} tok/s")
+    host = {k: round(float(v) / max(args.steps - 1, 1) / 1e3, 2)
+            for k, v in zip(("build_us", "init_upload_us", "run_us", "free_us"), phase_ns)}
+    log(f"decode: {args.steps} steps in {decode_s:.3f} s = {tps:.1f} tok/s; per step {host}")
 
-    # per-kernel timing pass: direct launches, one hipEvent pair per launch on the library's stream
-    ctx.set_timing(True)
-    ctx.reset_kernel_stats()
-    kv_begin = pos
-    for _ in range(args.timing_steps):
-        tok = int(model.step([tok], pos)[-1])
-        pos += 1
-    ctx.sync()
-    stats = ctx.kernel_stats()
-    ctx.set_timing(False)
-    kv_mid = (kv_begin + pos) // 2 + 1
+    # device time per token: replays of the captured decode graph, back to back, no host work in between
+    replay_ns = model.time_kernel("decode_step", args.timing_steps)
+    log(f"decode graph replay: {replay_ns / 1e3:.1f} us per token = {1e9 / replay_ns:.1f} tok/s")
+
+    # per-kernel durations: back-to-back launches between one hipEvent pair on the library's stream
+    kv_mid = pos
     nbytes = decode_bytes(SHAPE, kv_mid)
     kernels = {}
     step_kernel_ns = 0.0
-    for name, (n, ns) in sorted(stats.items(), key=lambda kv: -kv[1][1]):
-        avg_ns = ns / n
-        step_kernel_ns += ns / args.timing_steps
-        row = {"launches": n, "avg_us": round(avg_ns / 1e3, 3)}
+    small_attn = kv_mid <= ATTN_SMALL_MAX  # the library's default switch-over to the two-kernel attention
+    for name in ("fused_embed", "fused_qkv_rope", "fused_attn_small", "fused_attn_scores", "fused_attn_pv",
+                 "fused_o_resid", "fused_gateup", "fused_down_resid", "fused_logits", "fused_argmax"):
+        per_layer = name not in ("fused_embed", "fused_logits", "fused_argmax")
+        reps = 4 * SHAPE["n_layer"] if per_layer else 32
+        avg_ns = model.time_kernel(name, reps)
+        used = not ((name == "fused_attn_small" and not small_attn) or
+                    (name in ("fused_attn_scores", "fused_attn_pv") and small_attn))
+        if used:
+            step_kernel_ns += avg_ns * (SHAPE["n_layer"] if per_layer else 1)
+        row = {"avg_us": round(avg_ns / 1e3, 3)}
         if name in nbytes:
             row["GBps"] = round(nbytes[name] / avg_ns, 1)
         kernels[name] = row
-        log(f"  {name:20s} {n:6d} launches  avg {avg_ns / 1e3:9.2f} us  {row.get('GBps', '')}")
-    # the dominant kernel: back-to-back launches over the 32 layers' weights between one hipEvent pair
+        log(f"  {name:20s} avg {avg_ns / 1e3:9.2f} us  {row.get('GBps', '')}")
     dom = "fused_gateup"
-    dom_avg_ns = model.time_kernel(dom, 4 * SHAPE["n_layer"])
-    log(f"  {dom}: {dom_avg_ns / 1e3:.2f} us per back-to-back launch")
+    dom_avg_ns = kernels[dom]["avg_us"] * 1e3
     achieved = nbytes[dom] / dom_avg_ns  # GB/s
-    step_bytes = sum(v for k, v in nbytes.items() if k in ("fused_qkv_rope", "fused_attn_scores", "fused_o_resid",
-                                                           "fused_gateup", "fused_down_resid")) * SHAPE["n_layer"]
-    step_bytes += nbytes["fused_embed"] + nbytes["fused_logits"] + nbytes["fused_argmax"]
+    # bytes of the average timed step: the cache length at the middle of the timed steps
+    mean_bytes = decode_bytes(SHAPE, PROMPT_LEN + args.warmup + args.steps // 2 + 1)
+    step_bytes = sum(v for k, v in mean_bytes.items() if k in ("fused_qkv_rope", "fused_attn_scores", "fused_o_resid",
+                                                               "fused_gateup", "fused_down_resid")) * SHAPE["n_layer"]
+    step_bytes += mean_bytes["fused_embed"] + mean_bytes["fused_logits"] + mean_bytes["fused_argmax"]
     traffic = read_traffic(dom)
 
     result = {
@@ -231,6 +240,9 @@ def main():
         "decode_hbm_roofline_frac": round(step_bytes / (decode_s / args.steps) / 1e9 / HBM_PEAK_GBS, 4),
         "decode_bytes_per_token": step_bytes,
         "kernel_ms_per_step": round(step_kernel_ns / 1e6, 4),
+        "graph_replay_ms_per_step": round(replay_ns / 1e6, 4),
+        "graph_replay_tok_s": round(1e9 / replay_ns, 1),
+        "host_per_step": host,
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes": nbytes[dom], "avg_us": round(dom_avg_ns / 1e3, 3)},

@@ -37,9 +37,11 @@ extern vkllm_err_t vkllm_hip_reset_kernel_stats(struct vkllm_context *context);
 
 /* Launches the decode-step kernel `family` `reps` times back to back, cycling over the layers' weights, between
  * one hipEvent pair on the context's stream, and returns the elapsed nanoseconds: the kernel's duration without
- * the per-launch dispatch latency that a per-launch event pair adds. The kernel must leave the model's state
- * unchanged when repeated; supported: "fused_gateup" (RMSNorm + [Wu;Wg] GEMV + SwiGLU into a scratch buffer).
- * Needs a preceding single-token step of `model`. */
+ * the per-launch dispatch latency that a per-launch event pair adds. Families: "fused_embed", "fused_qkv_rope",
+ * "fused_attn_scores", "fused_attn_pv", "fused_attn_small", "fused_o_resid", "fused_gateup", "fused_down_resid",
+ * "fused_logits", "fused_argmax" (the embedding and residual GEMVs write into a scratch row, so repeats leave the
+ * model state unchanged), and "decode_step": replays of the captured single-token graph the last step used, at
+ * its position. Needs a preceding single-token step of `model`. */
 extern vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *context, struct vkllm_models_llama2 *model,
                                                const char *family, uint32_t reps, uint64_t *total_ns);
 
@@ -67,6 +69,18 @@ extern vkllm_err_t vkllm_models_llama2_init_random(struct vkllm_context *context
 /* Copies the fp16 logits [rows, vocab] of the model's last fused step into dst (rows <= that step's S). */
 extern vkllm_err_t vkllm_hip_model_last_logits(struct vkllm_context *context, struct vkllm_models_llama2 *model,
                                                uint16_t *dst, uint32_t rows);
+
+/* The reference driver's token loop (tests/vkllm_test_infer_gguf.c:181-272) in C: step 0 feeds `prompt`
+ * (prompt_len ids) at position `offset0`, every later step the previous step's last arg-max id at the next
+ * position. Each step runs vkllm_tensor_new(input_toks, mapped) -> vkllm_graph_new ->
+ * vkllm_models_llama2_build_graph -> vkllm_graph_init -> vkllm_commands_upload -> vkllm_graph_run ->
+ * vkllm_graph_post_run -> vkllm_tensor_invalid_cache -> read the last id -> vkllm_graph_free.
+ * ids[i] receives step i's last arg-max id, step_ns[i] (optional) the step's wall time, and phase_ns[4] (optional)
+ * the wall time summed over steps 1.. of: tensor_new + graph_new + build_graph; graph_init + upload;
+ * graph_run + post_run; invalid_cache + read + graph_free. */
+extern vkllm_err_t vkllm_hip_token_loop(struct vkllm_context *context, struct vkllm_models_llama2 *model,
+                                        const uint32_t *prompt, uint32_t prompt_len, uint32_t offset0,
+                                        uint32_t n_steps, uint32_t *ids, uint64_t *step_ns, uint64_t *phase_ns);
 
 /* Synchronise the context's stream. */
 extern vkllm_err_t vkllm_hip_synchronize(struct vkllm_context *context);

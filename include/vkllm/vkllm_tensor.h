@@ -35,6 +35,8 @@ struct vkllm_tensor
         bool is_ref;   /* view: memory is srcs[0]'s, never freed here */
         bool borrowed; /* memory owned elsewhere (model weight slab), never freed here */
         bool valid;    /* device contents have been written (upload or op) */
+        bool host_current; /* the host mirror holds the current contents (a fused step's arg-max output),
+                              so invalid_cache and download read it without a device copy */
     } data;
 
     uint32_t access_flags;   /* kept for source compatibility; unused */

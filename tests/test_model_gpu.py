@@ -144,3 +144,40 @@ def test_tokenizer(ctx, vk, tiny_gguf):
         assert model.tokenize("") == []
     finally:
         model.close()
+
+
+def _gpu_vs_oracle(ctx, vk, oracle, shape, seed, prompt_len, n_steps, prompt_seed):
+    """Greedy loop of a device-initialised model against the oracle's loop on the same seeded weights."""
+    cfg = oracle.make_cfg(**shape)
+    ref = oracle.Model(cfg=cfg, seed=seed)
+    prompt = oracle.prompt_tokens(prompt_seed, prompt_len, cfg.vocab)
+    want_ids, want_logits = ref.token_loop(prompt, n_steps, want_logits=True)
+    ref.close()
+    vcfg = vk.llama_config(shape["n_layer"], shape["dim"], shape["n_head"], shape["ffn"], shape["vocab"],
+                           shape["ctx"])
+    model = vk.Model(ctx, config=vcfg, seed=seed)
+    try:
+        ids, logits = model.token_loop(prompt, n_steps, want_logits=True)
+    finally:
+        model.close()
+    err = np.max(np.abs(logits.astype(np.float32) - want_logits.astype(np.float32)), axis=1)
+    print(f"max|dlogit| per step max {err.max():.3g} mean {err.mean():.3g}")
+    return ids, want_ids, err
+
+
+def test_7b_widths_two_layers(ctx, vk, oracle):
+    """The LLaMA-2-7B widths (dim 4096, 32 heads of 128, FFN 11008, vocab 32000) on two layers: the decode GEMVs,
+    attention and logits at their real shapes. 8-token prefill, then 6 greedy steps."""
+    shape = dict(n_layer=2, dim=4096, n_head=32, ffn=11008, vocab=32000, ctx=64)
+    ids, want_ids, err = _gpu_vs_oracle(ctx, vk, oracle, shape, seed=3, prompt_len=8, n_steps=6, prompt_seed=4)
+    assert err.max() <= LOGIT_TOL
+    assert ids.tolist() == want_ids.tolist()
+
+
+def test_long_context_decode(ctx, vk, oracle):
+    """Decode attention split over many cache chunks: head_dim 128, a 1000-token prompt, then 8 steps at kv 1001+
+    (63 chunks of 16 positions per head, merged by the last chunk's block)."""
+    shape = dict(n_layer=2, dim=256, n_head=2, ffn=512, vocab=1000, ctx=2048)
+    ids, want_ids, err = _gpu_vs_oracle(ctx, vk, oracle, shape, seed=5, prompt_len=1000, n_steps=8, prompt_seed=6)
+    assert err.max() <= LOGIT_TOL
+    assert ids.tolist() == want_ids.tolist()

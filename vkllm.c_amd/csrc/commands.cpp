@@ -53,6 +53,7 @@ void commands_note_write(vkllm_commands *cmds, vkllm_tensor *t)
 {
     vkllm_tensor *b = tensor_base(t);
     b->data.valid = true;
+    b->data.host_current = false;
     if (!b->data.mapped || !cmds)
         return;
     for (size_t i = 0; i < cmds->written_mapped->used_n; ++i)
@@ -88,6 +89,12 @@ extern "C" vkllm_err_t vkllm_commands_download(struct vkllm_context *context, st
     _CHECK_ARGS(context && commands && tensor && data);
     _CHECK_ARGS(bytes <= tensor->bytes);
     vkllm_tensor *b = tensor_base(tensor);
+    if (b->data.host_current && b->data.host)
+    {
+        HIP_TRY(hipStreamSynchronize(context->device->stream));
+        memcpy(data, b->data.host, bytes);
+        return VKLLM_ERR_OK;
+    }
     if (!b->data.valid)
     {
         log_error("tensor %s has no device contents (never written, or an intermediate of a fused step; set "

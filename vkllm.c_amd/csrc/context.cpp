@@ -203,7 +203,7 @@ static const char *kernel_names[KID_COUNT] = {
     "rope",          "softmax",       "ffn_up_and_gate", "update_rows",   "arg_max",       "fused_embed",
     "fused_qkv_rope", "fused_attn_scores", "fused_attn_pv", "fused_o_resid", "fused_gateup", "fused_down_resid",
     "fused_logits",  "fused_argmax",  "fused_rmsnorm",   "fused_gemm",    "fused_rope_kv", "fused_attn_prefill",
-    "fused_swiglu"};
+    "fused_swiglu",   "fused_attn_small"};
 
 vkllm_pipeline *pipeline_of(vkllm_context *ctx, KernelId id)
 {
@@ -349,6 +349,10 @@ extern "C" vkllm_err_t vkllm_context_new(uint32_t dev, struct vkllm_context **co
         return VKLLM_ERR_DEV_NOT_FOUND;
     }
     HIP_TRY(hipSetDevice((int)dev));
+    // host waits on the stream spin rather than sleep: a token step is milliseconds long and waking a sleeping
+    // waiter adds tens of microseconds to every step (VKLLM_SPIN_WAIT=0 keeps HIP's default scheduling)
+    if (env_flag("VKLLM_SPIN_WAIT", 1) && hipSetDeviceFlags(hipDeviceScheduleSpin) != hipSuccess)
+        (void)hipGetLastError(); // flags are fixed once the device is in use; keep what it has
     auto *ctx = (vkllm_context *)calloc(1, sizeof(vkllm_context));
     if (!ctx)
         return VKLLM_ERR_ALLOC;

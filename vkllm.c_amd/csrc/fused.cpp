@@ -2,16 +2,19 @@
 //
 // The graph keeps the reference's node structure (src/models/vkllm_models_llama2.c:488-602); its plan records
 // (model, input ids, offset, S). Running the plan:
-//   S == 1  the decode step: embed, 5 fused kernels per layer, logits, arg max. Kernels read the position from a
+//   S == 1  the decode step: embed, 6 fused kernels per layer, logits, arg max. Kernels read the position from a
 //           device-resident Step, so the whole sequence is captured once per model as a hipGraph and replayed for
-//           every token; only the token id and position are copied in before each replay.
+//           every token. The token id and position reach the device through a coherent pinned host block that
+//           the first kernel reads; the arg max writes the chosen id back into it, so no copy is queued.
 //   S >  1  prefill: embed, per layer RMSNorm -> QKV GEMM (MFMA) -> RoPE + KV append -> attention -> Wo GEMM with
 //           the residual add -> RMSNorm -> [up;gate] GEMM with SiLU on the gate half -> up*gate -> Wd GEMM with
 //           the residual add; then RMSNorm -> logits GEMM for all S rows -> arg max per row.
 // Either way the S arg-max ids land in the mapped output tensor, as the reference's ARG_MAX node leaves them.
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <ctime>
 
 #include "model_priv.h"
 
@@ -31,11 +34,29 @@ struct FusedState
     uint32_t *ids = nullptr, *toks = nullptr;
     vk::Step *step = nullptr;    // device
     vk::Step *step_h = nullptr;  // pinned staging for step + first token
-    uint32_t *io_h = nullptr;    // pinned: [0] token for decode, then ids read back
+    uint32_t *io_h = nullptr;    // pinned: a prefill's ids, uploaded and read back
+    vk::DecodeIo *dio = nullptr; // pinned, coherent: a single-token step's position, token and arg-max id
     float *freqs = nullptr;      // device copy of the RoPE denominators
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
+    // decode attention scratch: scores [H, ctx], chunk statistics [H, cmax, 2]
+    float *att_scores = nullptr, *att_stats = nullptr;
+    uint32_t att_cmax = 0;
+    // decode attention in one kernel up to this many positions, in two kernels beyond (VKLLM_ATTN_SMALL_MAX)
+    uint32_t attn_small_max = 0;
+    // captured single-token steps: [0] with the one-kernel attention, [1] with the two-kernel attention
+    hipGraph_t graph[2] = {nullptr, nullptr};
+    hipGraphExec_t exec[2] = {nullptr, nullptr};
+    int last_exec = -1;
+    // VKLLM_TRACE_HOST=1: host time of single-token steps spent enqueueing and waiting, printed at release
+    bool trace = false;
+    uint64_t trace_steps = 0, trace_enqueue_ns = 0, trace_wait_ns = 0;
 };
+
+static uint64_t host_ns()
+{
+    timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (uint64_t)ts.tv_sec * 1000000000ull + (uint64_t)ts.tv_nsec;
+}
 
 void *fused_plan_new(vkllm_models_llama2 *model, vkllm_tensor *input_toks, uint32_t offset)
 {
@@ -63,6 +84,20 @@ static void free_buffers(FusedState *fs)
     fs->cap_S = 0;
 }
 
+static void drop_graphs(FusedState *fs)
+{
+    for (int i = 0; i < 2; ++i)
+    {
+        if (fs->exec[i])
+            (void)hipGraphExecDestroy(fs->exec[i]);
+        if (fs->graph[i])
+            (void)hipGraphDestroy(fs->graph[i]);
+        fs->exec[i] = nullptr;
+        fs->graph[i] = nullptr;
+    }
+    fs->last_exec = -1;
+}
+
 void fused_model_release(vkllm_context *ctx, vkllm_models_llama2 *model)
 {
     ModelPriv *mp = model_priv(model);
@@ -70,19 +105,26 @@ void fused_model_release(vkllm_context *ctx, vkllm_models_llama2 *model)
         return;
     FusedState *fs = mp->fs;
     (void)hipStreamSynchronize(ctx->device->stream);
-    if (fs->exec)
-        (void)hipGraphExecDestroy(fs->exec);
-    if (fs->graph)
-        (void)hipGraphDestroy(fs->graph);
+    if (fs->trace && fs->trace_steps)
+        fprintf(stderr, "vkllm: %llu single-token steps: enqueue %.1f us, wait %.1f us per step\n",
+                (unsigned long long)fs->trace_steps, fs->trace_enqueue_ns / 1e3 / fs->trace_steps,
+                fs->trace_wait_ns / 1e3 / fs->trace_steps);
+    drop_graphs(fs);
     free_buffers(fs);
     if (fs->step)
         (void)hipFree(fs->step);
     if (fs->freqs)
         (void)hipFree(fs->freqs);
+    void *att[] = {fs->att_scores, fs->att_stats};
+    for (void *b : att)
+        if (b)
+            (void)hipFree(b);
     if (fs->step_h)
         (void)hipHostFree(fs->step_h);
     if (fs->io_h)
         (void)hipHostFree(fs->io_h);
+    if (fs->dio)
+        (void)hipHostFree(fs->dio);
     delete fs;
     mp->fs = nullptr;
 }
@@ -93,27 +135,33 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
     {
         mp->fs = new FusedState();
         FusedState *fs = mp->fs;
+        const char *tr = getenv("VKLLM_TRACE_HOST");
+        fs->trace = tr && *tr && *tr != '0';
         HIP_TRY(hipMalloc(&fs->step, sizeof(vk::Step)));
         HIP_TRY(hipHostMalloc((void **)&fs->step_h, sizeof(vk::Step), hipHostMallocDefault));
+        // read and written by the decode kernels in place: coherent, so no GPU cache holds a stale copy
+        HIP_TRY(hipHostMalloc((void **)&fs->dio, sizeof(vk::DecodeIo), hipHostMallocCoherent));
+        memset(fs->dio, 0, sizeof(vk::DecodeIo));
         HIP_TRY(hipMalloc(&fs->freqs, sizeof(float) * (mp->hd / 2 + 1)));
         HIP_TRY(hipMemcpyAsync(fs->freqs, mp->rope_freqs.data(), sizeof(float) * mp->hd / 2, hipMemcpyHostToDevice,
                                ctx->device->stream));
+        // decode attention: ceil(ctx / 32) chunks per head, at most 64; a chunk spans ceil(kv / chunks) positions
+        // rounded up to a multiple of 16
+        uint32_t cmax = (mp->ctx + 31) / 32;
+        fs->att_cmax = cmax > 64 ? 64 : cmax;
+        const size_t H = mp->H, C = fs->att_cmax;
+        const char *sm = getenv("VKLLM_ATTN_SMALL_MAX");
+        const uint32_t small = sm && *sm ? (uint32_t)strtoul(sm, nullptr, 10) : 1024u;
+        fs->attn_small_max = small < mp->ctx ? small : mp->ctx;
+        HIP_TRY(hipMalloc(&fs->att_scores, H * mp->ctx * sizeof(float)));
+        HIP_TRY(hipMalloc(&fs->att_stats, H * C * 2 * sizeof(float)));
     }
     FusedState *fs = mp->fs;
     if (S <= fs->cap_S)
         return VKLLM_ERR_OK;
-    // growing the activation buffers moves them: the captured decode graph refers to the old ones
+    // growing the activation buffers moves them: the captured decode graphs refer to the old ones
     HIP_TRY(hipStreamSynchronize(ctx->device->stream));
-    if (fs->exec)
-    {
-        (void)hipGraphExecDestroy(fs->exec);
-        fs->exec = nullptr;
-    }
-    if (fs->graph)
-    {
-        (void)hipGraphDestroy(fs->graph);
-        fs->graph = nullptr;
-    }
+    drop_graphs(fs);
     free_buffers(fs);
     if (fs->io_h)
     {
@@ -144,39 +192,29 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
             return hip_fail(_e, #_call, __FILE__, __LINE__);                                                        \
     } while (0)
 
-// RMSNorm(h) -> [Wu;Wg] GEMV -> up * silu(gate) into act, for layer l of a decode step
-static vk::GemvArgs gateup_args(const ModelPriv *mp, uint32_t l)
-{
-    vk::GemvArgs gu{};
-    gu.x = mp->fs->h;
-    gu.norm_w = mp->layers[l].ffn_norm;
-    gu.eps = mp->eps;
-    gu.w = mp->layers[l].wug;
-    gu.K = mp->D;
-    gu.rows = 2 * mp->F;
-    gu.units = mp->F;
-    gu.out = mp->fs->act;
-    return gu;
-}
-
-// decode: S == 1, position from fs->step
-static vkllm_err_t enqueue_decode(vkllm_context *ctx, ModelPriv *mp)
+// One launch of the decode step's kernel family `kid` (KID_F_*) for layer l. The embedding and the residual GEMVs
+// write the residual stream in place, or into `resid_out` when it is given (repeatable timing launches).
+static hipError_t launch_decode_kernel(vkllm_context *ctx, ModelPriv *mp, KernelId kid, uint32_t l,
+                                       uint16_t *resid_out = nullptr)
 {
     FusedState *fs = mp->fs;
     hipStream_t st = ctx->device->stream;
     const int cu = ctx->device->cu_count;
     const uint32_t D = mp->D, F = mp->F, V = mp->V, hd = mp->hd;
-    const float scale = 1.0f / sqrtf((float)hd);
-    KTRY(ctx, KID_F_EMBED, vk::launch_embed_rows(st, fs->toks, 1, mp->embd, fs->h, V, D, mp->pad_id));
-    for (uint32_t l = 0; l < mp->L; ++l)
+    const ModelPriv::Layer &ly = mp->layers[l];
+    vk::GemvArgs g{};
+    g.eps = mp->eps;
+    g.K = D;
+    switch (kid)
     {
-        const ModelPriv::Layer &ly = mp->layers[l];
-        vk::GemvArgs g{};
+    case KID_F_EMBED:
+        return vk::launch_embed_decode(st, fs->dio, fs->step, mp->embd, resid_out ? resid_out : fs->h, V, D,
+                                       mp->pad_id);
+    case KID_F_QKV:
+        // RMSNorm(h) -> [Wq;Wk;Wv] -> RoPE(q, k); q to fs->q, k and v into the caches at the step's position
         g.x = fs->h;
         g.norm_w = ly.attn_norm;
-        g.eps = mp->eps;
         g.w = ly.wqkv;
-        g.K = D;
         g.rows = 3 * D;
         g.units = 3 * D / 2;
         g.out = fs->q;
@@ -187,40 +225,86 @@ static vkllm_err_t enqueue_decode(vkllm_context *ctx, ModelPriv *mp)
         g.D = D;
         g.hd = hd;
         g.ctx = mp->ctx;
-        KTRY(ctx, KID_F_QKV, vk::launch_gemv(st, vk::EPI_QKV, g, cu));
-        KTRY(ctx, KID_F_ATTN_SCORES,
-             vk::launch_attn_decode(st, fs->q, ly.kc, ly.vc, fs->attn, fs->step, mp->H, hd, mp->ctx, scale));
-        vk::GemvArgs o{};
-        o.x = fs->attn;
-        o.w = ly.wo;
-        o.K = D;
-        o.rows = D;
-        o.units = (D + 1) / 2;
-        o.out = fs->h;
-        o.resid = fs->h;
-        KTRY(ctx, KID_F_O_RESID, vk::launch_gemv(st, vk::EPI_RESID, o, cu));
-        KTRY(ctx, KID_F_GATEUP, vk::launch_gemv(st, vk::EPI_GATEUP, gateup_args(mp, l), cu));
-        vk::GemvArgs dn{};
-        dn.x = fs->act;
-        dn.w = ly.wd;
-        dn.K = F;
-        dn.rows = D;
-        dn.units = (D + 1) / 2;
-        dn.out = fs->h;
-        dn.resid = fs->h;
-        KTRY(ctx, KID_F_DOWN_RESID, vk::launch_gemv(st, vk::EPI_RESID, dn, cu));
+        return vk::launch_gemv(st, vk::EPI_QKV, g, cu);
+    case KID_F_ATTN_SCORES:
+    case KID_F_ATTN_PV:
+    case KID_F_ATTN_SMALL:
+    {
+        vk::AttnDecodeArgs at{};
+        at.q = fs->q;
+        at.kc = ly.kc;
+        at.vc = ly.vc;
+        at.out = fs->attn;
+        at.step = fs->step;
+        at.scores = fs->att_scores;
+        at.stats = fs->att_stats;
+        at.H = mp->H;
+        at.hd = hd;
+        at.ctx = mp->ctx;
+        at.cmax = fs->att_cmax;
+        at.groups = vk::attn_pv_groups(mp->H, hd);
+        at.scale = 1.0f / sqrtf((float)hd);
+        if (kid == KID_F_ATTN_SMALL)
+            return vk::launch_attn_small(st, at, fs->attn_small_max);
+        return kid == KID_F_ATTN_SCORES ? vk::launch_attn_scores(st, at) : vk::launch_attn_pv(st, at);
     }
-    vk::GemvArgs lg{};
-    lg.x = fs->h;
-    lg.norm_w = mp->out_norm;
-    lg.eps = mp->eps;
-    lg.w = mp->out_w;
-    lg.K = D;
-    lg.rows = V;
-    lg.units = (V + 1) / 2;
-    lg.out = fs->logits;
-    KTRY(ctx, KID_F_LOGITS, vk::launch_gemv(st, vk::EPI_PLAIN, lg, cu));
-    KTRY(ctx, KID_F_ARGMAX, vk::launch_argmax_rows(st, fs->logits, fs->ids, 1, V));
+    case KID_F_O_RESID:
+    case KID_F_DOWN_RESID:
+        // h + W x, x the attention output (Wo) or up * silu(gate) (Wd)
+        g.x = kid == KID_F_O_RESID ? fs->attn : fs->act;
+        g.w = kid == KID_F_O_RESID ? ly.wo : ly.wd;
+        g.K = kid == KID_F_O_RESID ? D : F;
+        g.rows = D;
+        g.units = (D + 1) / 2;
+        g.out = resid_out ? resid_out : fs->h;
+        g.resid = fs->h;
+        return vk::launch_gemv(st, vk::EPI_RESID, g, cu);
+    case KID_F_GATEUP:
+        // RMSNorm(h) -> [Wu;Wg] -> up * silu(gate) into fs->act
+        g.x = fs->h;
+        g.norm_w = ly.ffn_norm;
+        g.w = ly.wug;
+        g.rows = 2 * F;
+        g.units = F;
+        g.out = fs->act;
+        return vk::launch_gemv(st, vk::EPI_GATEUP, g, cu);
+    case KID_F_LOGITS:
+        g.x = fs->h;
+        g.norm_w = mp->out_norm;
+        g.w = mp->out_w;
+        g.rows = V;
+        g.units = (V + 1) / 2;
+        g.out = fs->logits;
+        return vk::launch_gemv(st, vk::EPI_PLAIN, g, cu);
+    case KID_F_ARGMAX:
+        return vk::launch_argmax_rows(st, fs->logits, fs->ids, 1, V, fs->dio);
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
+#define DTRY(_ctx, _mp, _kid, _l) KTRY(_ctx, _kid, launch_decode_kernel((_ctx), (_mp), (_kid), (_l)))
+
+// decode: S == 1, position from fs->step; `small_attn` picks the one-kernel attention (kv <= attn_small_max)
+static vkllm_err_t enqueue_decode(vkllm_context *ctx, ModelPriv *mp, bool small_attn)
+{
+    DTRY(ctx, mp, KID_F_EMBED, 0);
+    for (uint32_t l = 0; l < mp->L; ++l)
+    {
+        DTRY(ctx, mp, KID_F_QKV, l);
+        if (small_attn)
+            DTRY(ctx, mp, KID_F_ATTN_SMALL, l);
+        else
+        {
+            DTRY(ctx, mp, KID_F_ATTN_SCORES, l);
+            DTRY(ctx, mp, KID_F_ATTN_PV, l);
+        }
+        DTRY(ctx, mp, KID_F_O_RESID, l);
+        DTRY(ctx, mp, KID_F_GATEUP, l);
+        DTRY(ctx, mp, KID_F_DOWN_RESID, l);
+    }
+    DTRY(ctx, mp, KID_F_LOGITS, 0);
+    DTRY(ctx, mp, KID_F_ARGMAX, 0);
     return VKLLM_ERR_OK;
 }
 
@@ -261,12 +345,6 @@ vkllm_err_t fused_plan_init(vkllm_context *ctx, vkllm_graph *graph)
     _CHECK_ARGS(mp && mp->fused_ok);
     _CHECK_ARGS(p->offset + p->S <= mp->ctx);
     _CHECK_ARGS(p->input_toks->dtype == vkllm_dtype_uint32 && p->input_toks->data.mapped);
-    // decode attention keeps a whole row of scores in LDS next to an 8 KB reduction buffer
-    if (p->S == 1 && (size_t)mp->ctx * sizeof(float) > 54 * 1024)
-    {
-        log_error("fused decode supports context_length <= %u", (unsigned)(54 * 1024 / sizeof(float)));
-        return VKLLM_ERR_ARGS;
-    }
     if (p->S > 1 && (size_t)(p->offset + p->S) * sizeof(float) > 60 * 1024)
     {
         log_error("prefill attention holds %u scores per row in LDS; at most %u", p->offset + p->S,
@@ -284,20 +362,24 @@ vkllm_err_t fused_plan_run(vkllm_context *ctx, vkllm_graph *graph)
     FusedState *fs = mp->fs;
     hipStream_t st = ctx->device->stream;
     const uint32_t S = p->S;
-    // step inputs: ids from the mapped input tensor's host mirror (written by vkllm_commands_upload)
-    fs->step_h->offset = p->offset;
-    fs->step_h->S = S;
-    memcpy(fs->io_h, p->input_toks->data.host, (size_t)S * 4);
-    HIP_TRY(hipMemcpyAsync(fs->step, fs->step_h, sizeof(vk::Step), hipMemcpyHostToDevice, st));
-    HIP_TRY(hipMemcpyAsync(fs->toks, fs->io_h, (size_t)S * 4, hipMemcpyHostToDevice, st));
+    // the step's ids are in the mapped input tensor's host mirror (written by vkllm_commands_upload)
+    const uint32_t *toks = (const uint32_t *)p->input_toks->data.host;
+    vkllm_tensor *out = graph->output_node;
     if (S == 1)
     {
+        // position and token go through the pinned block that the step's first kernel reads; the arg max writes
+        // the chosen id back into it
+        fs->dio->offset = p->offset;
+        fs->dio->token = toks[0];
+        const uint64_t t0 = fs->trace ? host_ns() : 0;
+        const bool small = p->offset + 1 <= fs->attn_small_max;
         if (ctx->device->graph_replay && !ctx->device->timing)
         {
-            if (!fs->exec)
+            const int v = small ? 0 : 1;
+            if (!fs->exec[v])
             {
                 HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
-                vkllm_err_t rc = enqueue_decode(ctx, mp);
+                vkllm_err_t rc = enqueue_decode(ctx, mp, small);
                 hipGraph_t g = nullptr;
                 hipError_t ce = hipStreamEndCapture(st, &g);
                 if (rc != VKLLM_ERR_OK)
@@ -307,27 +389,49 @@ vkllm_err_t fused_plan_run(vkllm_context *ctx, vkllm_graph *graph)
                     return rc;
                 }
                 HIP_TRY(ce);
-                fs->graph = g;
-                HIP_TRY(hipGraphInstantiate(&fs->exec, g, nullptr, nullptr, 0));
+                fs->graph[v] = g;
+                HIP_TRY(hipGraphInstantiate(&fs->exec[v], g, nullptr, nullptr, 0));
             }
-            HIP_TRY(hipGraphLaunch(fs->exec, st));
+            HIP_TRY(hipGraphLaunch(fs->exec[v], st));
+            fs->last_exec = v;
         }
         else
-            _CHECK(enqueue_decode(ctx, mp));
+            _CHECK(enqueue_decode(ctx, mp, small));
+        const uint64_t t1 = fs->trace ? host_ns() : 0;
+        HIP_TRY(hipStreamSynchronize(st));
+        fs->io_h[0] = ((volatile vk::DecodeIo *)fs->dio)->id;
+        if (fs->trace)
+        {
+            fs->trace_steps += 1;
+            fs->trace_enqueue_ns += t1 - t0;
+            fs->trace_wait_ns += host_ns() - t1;
+        }
     }
     else
+    {
+        fs->step_h->offset = p->offset;
+        fs->step_h->S = S;
+        memcpy(fs->io_h, toks, (size_t)S * 4);
+        HIP_TRY(hipMemcpyAsync(fs->step, fs->step_h, sizeof(vk::Step), hipMemcpyHostToDevice, st));
+        HIP_TRY(hipMemcpyAsync(fs->toks, fs->io_h, (size_t)S * 4, hipMemcpyHostToDevice, st));
         _CHECK(enqueue_prefill(ctx, mp, S, p->offset));
-    // results: arg-max ids into the output node's device memory and host mirror
-    vkllm_tensor *out = graph->output_node;
+        HIP_TRY(hipMemcpyAsync(fs->io_h, fs->ids, (size_t)S * 4, hipMemcpyDeviceToHost, st));
+        HIP_TRY(hipStreamSynchronize(st));
+    }
+    // results: the arg-max ids into the output node, as the reference's mapped ARG_MAX output holds them
+    if (out->data.host)
+    {
+        memcpy(out->data.host, fs->io_h, (size_t)S * 4);
+        out->data.host_current = true;
+        out->data.valid = false;
+        return VKLLM_ERR_OK;
+    }
     void *out_dev = tensor_dev(ctx, out);
     if (!out_dev)
         return VKLLM_ERR_ALLOC;
     HIP_TRY(hipMemcpyAsync(out_dev, fs->ids, (size_t)S * 4, hipMemcpyDeviceToDevice, st));
-    HIP_TRY(hipMemcpyAsync(fs->io_h, fs->ids, (size_t)S * 4, hipMemcpyDeviceToHost, st));
     HIP_TRY(hipStreamSynchronize(st));
     out->data.valid = true;
-    if (out->data.host)
-        memcpy(out->data.host, fs->io_h, (size_t)S * 4);
     return VKLLM_ERR_OK;
 }
 
@@ -352,11 +456,37 @@ extern "C" vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *ctx, st
     _CHECK_ARGS(ctx && model && family && reps > 0 && total_ns);
     ModelPriv *mp = model_priv(model);
     _CHECK_ARGS(mp && mp->fs && mp->fs->cap_S >= 1 && mp->fs->h);
-    _CHECK_ARGS(strcmp(family, "fused_gateup") == 0);
+    FusedState *fs = mp->fs;
+    static const struct
+    {
+        const char *name;
+        KernelId kid;
+    } families[] = {{"fused_embed", KID_F_EMBED},         {"fused_qkv_rope", KID_F_QKV},
+                    {"fused_attn_scores", KID_F_ATTN_SCORES}, {"fused_attn_pv", KID_F_ATTN_PV},
+                    {"fused_attn_small", KID_F_ATTN_SMALL},
+                    {"fused_o_resid", KID_F_O_RESID},     {"fused_gateup", KID_F_GATEUP},
+                    {"fused_down_resid", KID_F_DOWN_RESID}, {"fused_logits", KID_F_LOGITS},
+                    {"fused_argmax", KID_F_ARGMAX}};
+    const bool whole = strcmp(family, "decode_step") == 0;
+    int kid = -1;
+    for (const auto &f : families)
+        if (strcmp(family, f.name) == 0)
+            kid = f.kid;
+    _CHECK_ARGS(whole || kid >= 0);
+    if (whole && fs->last_exec < 0)
+    {
+        log_error("decode_step timing needs a captured decode step (graph replay on, one single-token step run)");
+        return VKLLM_ERR_ARGS;
+    }
     hipStream_t st = ctx->device->stream;
-    const int cu = ctx->device->cu_count;
+    // the residual GEMVs write into fs->xn (a scratch row) so that repeating them leaves the model state unchanged
+    auto launch = [&](uint32_t r) -> hipError_t {
+        if (whole)
+            return hipGraphLaunch(fs->exec[fs->last_exec], st);
+        return launch_decode_kernel(ctx, mp, (KernelId)kid, r % mp->L, fs->xn);
+    };
     // one untimed launch so the first timed one does not pay for code loading
-    HIP_TRY(vk::launch_gemv(st, vk::EPI_GATEUP, gateup_args(mp, 0), cu));
+    HIP_TRY(launch(0));
     hipEvent_t ev[2];
     HIP_TRY(hipEventCreate(&ev[0]));
     if (hipEventCreate(&ev[1]) != hipSuccess)
@@ -366,7 +496,7 @@ extern "C" vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *ctx, st
     }
     hipError_t e = hipEventRecord(ev[0], st);
     for (uint32_t r = 0; r < reps && e == hipSuccess; ++r)
-        e = vk::launch_gemv(st, vk::EPI_GATEUP, gateup_args(mp, (r + 1) % mp->L), cu);
+        e = launch(r + 1);
     if (e == hipSuccess)
         e = hipEventRecord(ev[1], st);
     if (e == hipSuccess)

@@ -101,11 +101,11 @@ static bool use_fused(vkllm_context *ctx, vkllm_graph *g)
 extern "C" vkllm_err_t vkllm_graph_init(struct vkllm_context *context, struct vkllm_graph *graph)
 {
     _CHECK_ARGS(context && graph && graph->output_node && graph->commands);
-    _CHECK(visit_post_order(graph->output_node,
-                            [&](vkllm_tensor *t) { return op_init(context, graph->commands, t); }));
+    // a fused step runs none of the node kernels: its plan validates what the fused kernels need instead
     if (use_fused(context, graph))
         return fused_plan_init(context, graph);
-    return VKLLM_ERR_OK;
+    return visit_post_order(graph->output_node,
+                            [&](vkllm_tensor *t) { return op_init(context, graph->commands, t); });
 }
 
 extern "C" vkllm_err_t vkllm_graph_run(struct vkllm_context *context, struct vkllm_graph *graph)
@@ -125,6 +125,9 @@ extern "C" vkllm_err_t vkllm_graph_run(struct vkllm_context *context, struct vkl
 extern "C" vkllm_err_t vkllm_graph_post_run(struct vkllm_context *context, struct vkllm_graph *graph)
 {
     _CHECK_ARGS(context && graph && graph->output_node && graph->commands);
+    // a fused step ran none of the node kernels, so there is no per-node post-run work
+    if (use_fused(context, graph))
+        return VKLLM_ERR_OK;
     return visit_post_order(graph->output_node,
                             [&](vkllm_tensor *t) { return op_post_run(context, graph->commands, t); });
 }

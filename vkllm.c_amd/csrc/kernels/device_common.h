@@ -130,4 +130,23 @@ __device__ __forceinline__ float silu(float v)
     return v / (1.0f + expf(-v));
 }
 
+// Order of the reference's ARG_MAX (src/shaders/vkllm_arg_max.comp:40-97). There, lane l of 32 keeps the first
+// maximum among elements i == l (mod 32) (strict '>'), then a strict-'>' tree over lane strides 16, 8, 4, 2, 1 keeps
+// the lower lane on ties, so lane bit 0 decides first, then bit 1, and so on. Among equal maxima the winner is the
+// index whose lane has the smallest 5-bit bit reversal, then the smallest index. As a comparison of (value, index)
+// pairs that is a total order, so a reduction in any grouping returns the reference's answer.
+__device__ __forceinline__ uint32_t lane_rank(uint32_t i)
+{
+    return __brev(i & 31u) >> 27;
+}
+
+// true when (v, i) comes before (w, k) in that order
+__device__ __forceinline__ bool am_before(float v, uint32_t i, float w, uint32_t k)
+{
+    if (v != w)
+        return v > w;
+    const uint32_t ri = lane_rank(i), rk = lane_rank(k);
+    return ri != rk ? ri < rk : i < k;
+}
+
 } // namespace vk

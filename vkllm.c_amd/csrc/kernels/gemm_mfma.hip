@@ -46,20 +46,22 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint16_t *__restrict__ 
             acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
     u32x4g ra[AV], rb[BV];
+    // unconditional loads at clamped addresses (a guarded load compiles to a branch and a wait per load): rows
+    // past M or N only feed outputs that are not stored; K columns past the end are zeroed by a select
     auto load = [&](uint32_t k0) {
 #pragma unroll
         for (int i = 0; i < AV; ++i)
         {
-            const uint32_t v = tid + 256 * i, row = v / 4, kk = k0 + (v % 4) * 8;
-            ra[i] = (m0 + row < M && kk < K) ? *(const u32x4g *)(A + (size_t)(m0 + row) * K + kk)
-                                               : (u32x4g){0, 0, 0, 0};
+            const uint32_t v = tid + 256 * i, row = min(m0 + v / 4, M - 1), kk = k0 + (v % 4) * 8;
+            const u32x4g x = *(const u32x4g *)(A + (size_t)row * K + min(kk, K - 8));
+            ra[i] = kk < K ? x : (u32x4g){0, 0, 0, 0};
         }
 #pragma unroll
         for (int i = 0; i < BV; ++i)
         {
-            const uint32_t v = tid + 256 * i, row = v / 4, kk = k0 + (v % 4) * 8;
-            rb[i] = (n0 + row < N && kk < K) ? *(const u32x4g *)(B + (size_t)(n0 + row) * K + kk)
-                                               : (u32x4g){0, 0, 0, 0};
+            const uint32_t v = tid + 256 * i, row = min(n0 + v / 4, N - 1), kk = k0 + (v % 4) * 8;
+            const u32x4g x = *(const u32x4g *)(B + (size_t)row * K + min(kk, K - 8));
+            rb[i] = kk < K ? x : (u32x4g){0, 0, 0, 0};
         }
     };
 

@@ -48,6 +48,18 @@ struct Step
     uint32_t S;      // tokens in the step
 };
 
+// Inputs and output of a single-token step in pinned host memory: the host writes the position and token before
+// the step, the first kernel copies them into the device Step, the arg max writes the chosen id back.
+struct DecodeIo
+{
+    uint32_t offset;
+    uint32_t token;
+    uint32_t id;
+    uint32_t pad;
+};
+// single-token step: step = {io->offset, 1}, h = embd[io->token] (ids >= V read row unk)
+hipError_t launch_embed_decode(hipStream_t st, const DecodeIo *io, Step *step, const uint16_t *embd, uint16_t *h,
+                               uint32_t V, uint32_t D, uint32_t unk);
 // h[s] = embd[toks[s]] (ids >= V read row unk), s < S; D % 8 == 0
 hipError_t launch_embed_rows(hipStream_t st, const uint32_t *toks, uint32_t S, const uint16_t *embd, uint16_t *h,
                              uint32_t V, uint32_t D, uint32_t unk);
@@ -70,7 +82,8 @@ struct GemvArgs
     float eps;
     const uint16_t *w;      // weight rows [rows, K], K contiguous
     uint32_t K;
-    uint32_t units;         // work units: PLAIN/RESID ceil(rows/2), GATEUP F, QKV 3D/2
+    uint32_t units;         // fallback kernel (K > 14336) work units: PLAIN/RESID ceil(rows/2), GATEUP F, QKV 3D/2
+    uint32_t rows_per_unit; // rows a wave reduces at once (1, 2 or 4); 0 picks the default for the shape
     uint32_t rows;          // weight rows
     uint16_t *out;
     const uint16_t *resid;  // EPI_RESID
@@ -82,11 +95,28 @@ struct GemvArgs
 };
 hipError_t launch_gemv(hipStream_t st, int epi, const GemvArgs &a, int cu_count);
 
-// single-token attention over the cache for every head, one workgroup per head:
-// s_j = fp16(scale q.k_j), p = fp16(softmax(s)), out[h*hd + d] = fp16(sum_j p_j v_j[d]); kv = step->offset + 1.
-// When kv == hd the product is p . V^T (the reference's shape-based transposition rule).
-hipError_t launch_attn_decode(hipStream_t st, const uint16_t *q, const uint16_t *kc, const uint16_t *vc,
-                              uint16_t *out, const Step *step, uint32_t H, uint32_t hd, uint32_t ctx, float scale);
+// single-token attention over the cache for every head (kv = step->offset + 1): s_j = fp16(scale q.k_j),
+// p = fp16(softmax(s)), out[h*hd + d] = fp16(sum_j p_j v_j[d]); when kv == hd the product is p . V^T (the
+// reference's shape-based transposition rule). Scores are split into at most `cmax` chunks per head (multiples of
+// 16 positions); the probability-weighted sum into `groups` slices of the head's dims (attn_pv_groups).
+struct AttnDecodeArgs
+{
+    const uint16_t *q;        // [H, hd]
+    const uint16_t *kc, *vc;  // [H, ctx, hd]
+    uint16_t *out;            // [H, hd]
+    const Step *step;
+    float *scores;            // [H, ctx]
+    float *stats;             // [H, cmax, 2]: chunk max, chunk sum of exp
+    uint32_t H, hd, ctx, cmax, groups;
+    float scale;
+};
+uint32_t attn_pv_groups(uint32_t H, uint32_t hd);
+hipError_t launch_attn_scores(hipStream_t st, const AttnDecodeArgs &a);
+hipError_t launch_attn_pv(hipStream_t st, const AttnDecodeArgs &a);
+// the same attention in one kernel that recomputes a head's scores in each of its `groups` blocks (no scores or
+// statistics scratch); for kv <= kv_max, which sizes its LDS
+hipError_t launch_attn_small(hipStream_t st, const AttnDecodeArgs &a, uint32_t kv_max);
+
 // prefill: queries s < S at positions offset+s attend to positions <= offset+s
 hipError_t launch_attn_prefill(hipStream_t st, const uint16_t *q, const uint16_t *kc, const uint16_t *vc,
                                uint16_t *out, uint32_t offset, uint32_t S, uint32_t H, uint32_t hd, uint32_t ctx,
@@ -96,8 +126,10 @@ hipError_t launch_rope_kv(hipStream_t st, const uint16_t *qkv, uint16_t *q, uint
                           const float *freqs, uint32_t offset, uint32_t S, uint32_t D, uint32_t hd, uint32_t ctx);
 // act[s][n] = fp16(ug[s][n] * ug[s][F + n])
 hipError_t launch_swiglu(hipStream_t st, const uint16_t *ug, uint16_t *act, uint32_t S, uint32_t F);
-// ids[s] = arg_max(logits[s]) with the reference's tie rule, contiguous rows of V
-hipError_t launch_argmax_rows(hipStream_t st, const uint16_t *logits, uint32_t *ids, uint32_t S, uint32_t V);
+// ids[s] = arg_max(logits[s]) with the reference's tie rule, contiguous rows of V; with `io`, row 0's id also goes
+// to io->id
+hipError_t launch_argmax_rows(hipStream_t st, const uint16_t *logits, uint32_t *ids, uint32_t S, uint32_t V,
+                              DecodeIo *io = nullptr);
 
 enum GemmEpi : int
 {

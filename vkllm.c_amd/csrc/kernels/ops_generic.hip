@@ -392,74 +392,62 @@ hipError_t launch_softmax(hipStream_t st, const TView &in, const TView &out, int
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// VKLLM_OP_ARG_MAX (src/shaders/vkllm_arg_max.comp:40-97). The reference's 32 lanes each keep the first maximum of
-// the elements i == lane (mod 32); lanes then merge with a strict '>' tree over strides 16..1 where the lower lane
-// keeps ties. Here 256 threads split each lane's elements (thread t sees i == t (mod 256), all in lane t % 32), the
-// per-lane partials merge with "larger value, then smaller index", and the 32-lane tree runs exactly as written.
+// VKLLM_OP_ARG_MAX (src/shaders/vkllm_arg_max.comp:40-97) on any strided view: each thread keeps the first element
+// of its share under the reference's arg-max order (am_before), then wave shuffles and one LDS step reduce the
+// row. Contiguous fp16 rows take the fused step's 16-byte-load kernel (launch_argmax_rows).
 __global__ __launch_bounds__(256) void arg_max_kernel(TView in, TView out)
 {
-    __shared__ float sv[256];
-    __shared__ uint32_t si[256];
-    __shared__ int sh[256];
+    __shared__ float wv[4];
+    __shared__ uint32_t wi[4];
     uint32_t b, c, h, w;
     const uint32_t n3[4] = {in.n[0], in.n[1], in.n[2], 1};
     unflatten(blockIdx.x, n3, b, c, h, w);
     const uint32_t W = in.n[3];
     const size_t row = voff(in, b, c, h, 0);
     const uint32_t t = threadIdx.x;
-    float bv = -FLT_MAX;
-    uint32_t bi = t % 32;
-    int have = 0;
-    if (t < 32)
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu; // no element: every element comes before it
+    for (uint32_t i = t; i < W; i += 256)
     {
-        have = 1;
-        if (t < W)
-            bv = ldf(in, row + (size_t)t * in.s[3]);
-    }
-    for (uint32_t i = (t < 32 ? t + 256 : t); i < W; i += 256)
-    {
-        float v = ldf(in, row + (size_t)i * in.s[3]);
-        if (!have || v > bv)
+        const float v = ldf(in, row + (size_t)i * in.s[3]);
+        if (am_before(v, i, bv, bi))
         {
             bv = v;
             bi = i;
-            have = 1;
         }
     }
-    sv[t] = bv;
-    si[t] = bi;
-    sh[t] = have;
-    __syncthreads();
-    if (t < 32)
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
     {
-        // merge the 8 threads of lane t (t, t+32, ..., t+224)
-        for (uint32_t k = t + 32; k < 256; k += 32)
+        const float v = __shfl_xor(bv, o, kWave);
+        const uint32_t i = (uint32_t)__shfl_xor((int)bi, o, kWave);
+        if (am_before(v, i, bv, bi))
         {
-            if (!sh[k])
-                continue;
-            if (sv[k] > bv || (sv[k] == bv && si[k] < bi))
-            {
-                bv = sv[k];
-                bi = si[k];
-            }
+            bv = v;
+            bi = i;
         }
-        sv[t] = bv;
-        si[t] = bi;
+    }
+    if ((t & 63) == 0)
+    {
+        wv[t >> 6] = bv;
+        wi[t >> 6] = bi;
     }
     __syncthreads();
     if (t == 0)
     {
-        for (uint32_t s = 16; s > 0; s >>= 1)
-            for (uint32_t l = 0; l < s; ++l)
-                if (sv[l + s] > sv[l])
-                {
-                    sv[l] = sv[l + s];
-                    si[l] = si[l + s];
-                }
-        const uint32_t o3[4] = {out.n[0], out.n[1], out.n[2], 1};
-        (void)o3;
-        ((uint32_t *)out.p)[voff(out, b, c, h, 0)] = si[0];
+        for (int k = 1; k < 4; ++k)
+            if (am_before(wv[k], wi[k], bv, bi))
+            {
+                bv = wv[k];
+                bi = wi[k];
+            }
+        ((uint32_t *)out.p)[voff(out, b, c, h, 0)] = bi;
     }
+}
+
+static bool contiguous(const TView &t)
+{
+    return t.s[3] == 1 && t.s[2] == t.n[3] && t.s[1] == t.n[2] * t.s[2] && t.s[0] == t.n[1] * t.s[1];
 }
 
 hipError_t launch_arg_max(hipStream_t st, const TView &in, const TView &out)
@@ -467,6 +455,8 @@ hipError_t launch_arg_max(hipStream_t st, const TView &in, const TView &out)
     uint64_t rows = (uint64_t)in.n[0] * in.n[1] * in.n[2];
     if (rows == 0)
         return hipSuccess;
+    if (in.dt == DT_F16 && contiguous(in) && contiguous(out))
+        return launch_argmax_rows(st, (const uint16_t *)in.p, (uint32_t *)out.p, (uint32_t)rows, in.n[3]);
     arg_max_kernel<<<(uint32_t)rows, 256, 0, st>>>(in, out);
     return hipGetLastError();
 }

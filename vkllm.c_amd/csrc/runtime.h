@@ -52,6 +52,7 @@ enum KernelId
     KID_F_ROPE_KV,
     KID_F_ATTN_PREFILL,
     KID_F_SWIGLU,
+    KID_F_ATTN_SMALL,
     KID_COUNT
 };
 

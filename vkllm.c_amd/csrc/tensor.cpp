@@ -162,7 +162,7 @@ extern "C" vkllm_err_t vkllm_tensor_invalid_cache(struct vkllm_context *context,
     void *dev = tensor_dev(context, b);
     if (!dev)
         return VKLLM_ERR_ALLOC;
-    if (b->data.valid)
+    if (b->data.valid && !b->data.host_current)
         HIP_TRY(hipMemcpyAsync(b->data.host, dev, b->bytes, hipMemcpyDeviceToHost, context->device->stream));
     HIP_TRY(hipStreamSynchronize(context->device->stream));
     return VKLLM_ERR_OK;

@@ -31,7 +31,8 @@ class VkllmError(RuntimeError):
 
 class TensorData(ctypes.Structure):
     _fields_ = [("dev", ctypes.c_void_p), ("host", ctypes.c_void_p), ("mapped", ctypes.c_bool),
-                ("is_ref", ctypes.c_bool), ("borrowed", ctypes.c_bool), ("valid", ctypes.c_bool)]
+                ("is_ref", ctypes.c_bool), ("borrowed", ctypes.c_bool), ("valid", ctypes.c_bool),
+                ("host_current", ctypes.c_bool)]
 
 
 class Tensor(ctypes.Structure):
@@ -212,6 +213,7 @@ def lib():
                                                 ctypes.POINTER(ctypes.c_uint64)]),
             "vkllm_hip_device_arch": (ctypes.c_char_p, [vp]),
             "vkllm_hip_model_last_logits": (E, [vp, ctypes.POINTER(ModelStruct), vp, u32]),
+            "vkllm_hip_token_loop": (E, [vp, ctypes.POINTER(ModelStruct), vp, u32, u32, u32, vp, vp, vp]),
             "vkllm_hip_abi_layout": (E, [ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_uint64), E]),
             "vkllm_hashmap_new": (E, [ctypes.POINTER(vp), ctypes.c_size_t]),
             "vkllm_hashmap_free": (None, [vp]),
@@ -493,6 +495,18 @@ class Model:
             return ids.copy()
         finally:
             L.vkllm_graph_free(ctx.vp, g)
+
+    def loop(self, prompt, n_steps, offset=0):
+        """The reference driver's loop run in C (vkllm_hip_token_loop): returns (ids [n_steps], per-step wall
+        nanoseconds [n_steps], phase nanoseconds summed over steps 1.. [build, init+upload, run, free])."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        ids = np.zeros(n_steps, np.uint32)
+        step_ns = np.zeros(n_steps, np.uint64)
+        phase_ns = np.zeros(4, np.uint64)
+        check("vkllm_hip_token_loop", lib().vkllm_hip_token_loop(
+            self.ctx.vp, ctypes.byref(self.m), prompt.ctypes.data, len(prompt), offset, n_steps, ids.ctypes.data,
+            step_ns.ctypes.data, phase_ns.ctypes.data))
+        return ids, step_ns, phase_ns
 
     def token_loop(self, prompt, n_steps, want_logits=False):
         """Prefill `prompt`, then feed back the arg max of the last row; n_steps ids (the first from prefill)."""
