@@ -36,7 +36,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 
 SHAPE = dict(n_layer=32, dim=4096, n_head=32, ffn=11008, vocab=32000)
 PROMPT_LEN = 128
-ATTN_SMALL_MAX = 1024  # positions up to which the decode attention is one kernel (VKLLM_ATTN_SMALL_MAX)
+ATTN_SMALL_MAX = 1536  # positions up to which the decode attention is one kernel (VKLLM_ATTN_SMALL_MAX)
 MODEL_SEED, PROMPT_SEED = 0, 1
 
 
@@ -184,8 +184,11 @@ def main():
     log(f"decode: {args.steps} steps in {decode_s:.3f} s = {tps:.1f} tok/s; per step {host}")
 
     # device time per token: replays of the captured decode graph, back to back, no host work in between
-    replay_ns = model.time_kernel("decode_step", args.timing_steps)
-    log(f"decode graph replay: {replay_ns / 1e3:.1f} us per token = {1e9 / replay_ns:.1f} tok/s")
+    # (not available when graph replay is switched off, e.g. VKLLM_GRAPH=0 under a kernel tracer)
+    replay_ns = None
+    if os.environ.get("VKLLM_GRAPH", "1") != "0":
+        replay_ns = model.time_kernel("decode_step", args.timing_steps)
+        log(f"decode graph replay: {replay_ns / 1e3:.1f} us per token = {1e9 / replay_ns:.1f} tok/s")
 
     # per-kernel durations: back-to-back launches between one hipEvent pair on the library's stream
     kv_mid = pos
@@ -240,8 +243,8 @@ def main():
         "decode_hbm_roofline_frac": round(step_bytes / (decode_s / args.steps) / 1e9 / HBM_PEAK_GBS, 4),
         "decode_bytes_per_token": step_bytes,
         "kernel_ms_per_step": round(step_kernel_ns / 1e6, 4),
-        "graph_replay_ms_per_step": round(replay_ns / 1e6, 4),
-        "graph_replay_tok_s": round(1e9 / replay_ns, 1),
+        "graph_replay_ms_per_step": round(replay_ns / 1e6, 4) if replay_ns else None,
+        "graph_replay_tok_s": round(1e9 / replay_ns, 1) if replay_ns else None,
         "host_per_step": host,
         "roofline": {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,

@@ -37,9 +37,10 @@ struct FusedState
     uint32_t *io_h = nullptr;    // pinned: a prefill's ids, uploaded and read back
     vk::DecodeIo *dio = nullptr; // pinned, coherent: a single-token step's position, token and arg-max id
     float *freqs = nullptr;      // device copy of the RoPE denominators
-    // decode attention scratch: scores [H, ctx], chunk statistics [H, cmax, 2]
-    float *att_scores = nullptr, *att_stats = nullptr;
-    uint32_t att_cmax = 0;
+    // decode attention scratch: scores [H, ctx], chunk statistics [H, cmax, 2], chunk partial sums [H, cmax, hd]
+    float *att_scores = nullptr, *att_stats = nullptr, *att_part = nullptr;
+    uint32_t *att_count = nullptr; // per-head chunk arrivals of the merge, zero between launches
+    uint32_t att_cmax = 0, att_chunk = 0;
     // decode attention in one kernel up to this many positions, in two kernels beyond (VKLLM_ATTN_SMALL_MAX)
     uint32_t attn_small_max = 0;
     // captured single-token steps: [0] with the one-kernel attention, [1] with the two-kernel attention
@@ -115,7 +116,7 @@ void fused_model_release(vkllm_context *ctx, vkllm_models_llama2 *model)
         (void)hipFree(fs->step);
     if (fs->freqs)
         (void)hipFree(fs->freqs);
-    void *att[] = {fs->att_scores, fs->att_stats};
+    void *att[] = {fs->att_scores, fs->att_stats, fs->att_part, fs->att_count};
     for (void *b : att)
         if (b)
             (void)hipFree(b);
@@ -145,16 +146,20 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         HIP_TRY(hipMalloc(&fs->freqs, sizeof(float) * (mp->hd / 2 + 1)));
         HIP_TRY(hipMemcpyAsync(fs->freqs, mp->rope_freqs.data(), sizeof(float) * mp->hd / 2, hipMemcpyHostToDevice,
                                ctx->device->stream));
-        // decode attention: ceil(ctx / 32) chunks per head, at most 64; a chunk spans ceil(kv / chunks) positions
-        // rounded up to a multiple of 16
-        uint32_t cmax = (mp->ctx + 31) / 32;
-        fs->att_cmax = cmax > 64 ? 64 : cmax;
+        // two-kernel decode attention: chunks of a fixed length of about 256 positions (a multiple of 16), each
+        // scored and summed by one block in a single round trip
+        const uint32_t cmax = (mp->ctx + 255) / 256;
+        fs->att_chunk = ((mp->ctx + cmax - 1) / cmax + 15) / 16 * 16;
+        fs->att_cmax = (mp->ctx + fs->att_chunk - 1) / fs->att_chunk;
         const size_t H = mp->H, C = fs->att_cmax;
         const char *sm = getenv("VKLLM_ATTN_SMALL_MAX");
-        const uint32_t small = sm && *sm ? (uint32_t)strtoul(sm, nullptr, 10) : 1024u;
+        const uint32_t small = sm && *sm ? (uint32_t)strtoul(sm, nullptr, 10) : 1536u;
         fs->attn_small_max = small < mp->ctx ? small : mp->ctx;
         HIP_TRY(hipMalloc(&fs->att_scores, H * mp->ctx * sizeof(float)));
         HIP_TRY(hipMalloc(&fs->att_stats, H * C * 2 * sizeof(float)));
+        HIP_TRY(hipMalloc(&fs->att_part, H * C * mp->hd * sizeof(float)));
+        HIP_TRY(hipMalloc(&fs->att_count, H * sizeof(uint32_t)));
+        HIP_TRY(hipMemset(fs->att_count, 0, H * sizeof(uint32_t)));
     }
     FusedState *fs = mp->fs;
     if (S <= fs->cap_S)
@@ -238,11 +243,14 @@ static hipError_t launch_decode_kernel(vkllm_context *ctx, ModelPriv *mp, Kernel
         at.step = fs->step;
         at.scores = fs->att_scores;
         at.stats = fs->att_stats;
+        at.part = fs->att_part;
+        at.count = fs->att_count;
         at.H = mp->H;
         at.hd = hd;
         at.ctx = mp->ctx;
         at.cmax = fs->att_cmax;
-        at.groups = vk::attn_pv_groups(mp->H, hd);
+        at.chunk = fs->att_chunk;
+        at.groups = vk::attn_groups(mp->H, hd, 8);
         at.scale = 1.0f / sqrtf((float)hd);
         if (kid == KID_F_ATTN_SMALL)
             return vk::launch_attn_small(st, at, fs->attn_small_max);

@@ -149,4 +149,98 @@ __device__ __forceinline__ bool am_before(float v, uint32_t i, float w, uint32_t
     return ri != rk ? ri < rk : i < k;
 }
 
+// ---- 16-byte vectors of fp16 pairs, dot products and DPP reductions ----
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float half_lo(uint32_t v)
+{
+    return h2f((uint16_t)(v & 0xffffu));
+}
+__device__ __forceinline__ float half_hi(uint32_t v)
+{
+    return h2f((uint16_t)(v >> 16));
+}
+
+// 8-element fp16 dot product accumulated in fp32 (fp16 -> fp32 widening FMAs, v_fma_mix_f32). The
+// v_dot2_f32_f16 builtin gave wrong sums on gfx950 and is not used.
+__device__ __forceinline__ float dot8(u32x4 w, u32x4 x, float acc)
+{
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        acc = fmaf(half_lo(w[i]), half_lo(x[i]), acc);
+        acc = fmaf(half_hi(w[i]), half_hi(x[i]), acc);
+    }
+    return acc;
+}
+__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi)
+{
+    return (uint32_t)lo | ((uint32_t)hi << 16);
+}
+
+// wave64 sum with DPP: row reductions (quad_perm, half-row and row mirrors), then row_bcast15/31 fold the four
+// rows into lane 63, which is broadcast with readlane.
+template <int ctrl, int row_mask> __device__ __forceinline__ float dpp_add(float v)
+{
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, row_mask, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v)
+{
+    v = dpp_add<0xB1, 0xF>(v);  // quad_perm [1,0,3,2]
+    v = dpp_add<0x4E, 0xF>(v);  // quad_perm [2,3,0,1]
+    v = dpp_add<0x141, 0xF>(v); // row_half_mirror
+    v = dpp_add<0x140, 0xF>(v); // row_mirror
+    v = dpp_add<0x142, 0xA>(v); // row_bcast:15 -> rows 1, 3
+    v = dpp_add<0x143, 0xC>(v); // row_bcast:31 -> rows 2, 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// sum over aligned groups of `lpk` lanes (1, 2, 4, 8 or 16) with in-row DPP; every lane gets its group's sum
+__device__ __forceinline__ float group_sum(float v, uint32_t lpk)
+{
+    if (lpk >= 2)
+        v = dpp_add<0xB1, 0xF>(v); // quad_perm [1,0,3,2]
+    if (lpk >= 4)
+        v = dpp_add<0x4E, 0xF>(v); // quad_perm [2,3,0,1]
+    if (lpk >= 8)
+        v = dpp_add<0x141, 0xF>(v); // row_half_mirror
+    if (lpk >= 16)
+        v = dpp_add<0x140, 0xF>(v); // row_mirror
+    return v;
+}
+
+template <int ctrl, int row_mask> __device__ __forceinline__ float dpp_max(float v)
+{
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), ctrl, row_mask,
+                                                               0xF, false)));
+}
+__device__ __forceinline__ float wave_max_dpp(float v)
+{
+    v = dpp_max<0xB1, 0xF>(v);
+    v = dpp_max<0x4E, 0xF>(v);
+    v = dpp_max<0x141, 0xF>(v);
+    v = dpp_max<0x140, 0xF>(v);
+    v = dpp_max<0x142, 0xA>(v);
+    v = dpp_max<0x143, 0xC>(v);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// reductions over the 4 waves of a 256-thread block; `red` holds 4 floats and is not reused by the other one
+__device__ __forceinline__ float block4_max(float v, float *red)
+{
+    v = wave_max_dpp(v);
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+__device__ __forceinline__ float block4_sum(float v, float *red)
+{
+    v = wave_sum_dpp(v);
+    if ((threadIdx.x & 63) == 0)
+        red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
 } // namespace vk

@@ -19,51 +19,6 @@
 namespace vk
 {
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ float half_lo(uint32_t v)
-{
-    return h2f((uint16_t)(v & 0xffffu));
-}
-__device__ __forceinline__ float half_hi(uint32_t v)
-{
-    return h2f((uint16_t)(v >> 16));
-}
-
-// 8-element fp16 dot product accumulated in fp32 (fp16 -> fp32 widening FMAs, v_fma_mix_f32). The
-// v_dot2_f32_f16 builtin gave wrong sums on gfx950 and is not used.
-__device__ __forceinline__ float dot8(u32x4 w, u32x4 x, float acc)
-{
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-    {
-        acc = fmaf(half_lo(w[i]), half_lo(x[i]), acc);
-        acc = fmaf(half_hi(w[i]), half_hi(x[i]), acc);
-    }
-    return acc;
-}
-__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi)
-{
-    return (uint32_t)lo | ((uint32_t)hi << 16);
-}
-
-// wave64 sum with DPP: row reductions (quad_perm, half-row and row mirrors), then row_bcast15/31 fold the four
-// rows into lane 63, which is broadcast with readlane.
-template <int ctrl, int row_mask> __device__ __forceinline__ float dpp_add(float v)
-{
-    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, row_mask, 0xF, false));
-}
-__device__ __forceinline__ float wave_sum_dpp(float v)
-{
-    v = dpp_add<0xB1, 0xF>(v);  // quad_perm [1,0,3,2]
-    v = dpp_add<0x4E, 0xF>(v);  // quad_perm [2,3,0,1]
-    v = dpp_add<0x141, 0xF>(v); // row_half_mirror
-    v = dpp_add<0x140, 0xF>(v); // row_mirror
-    v = dpp_add<0x142, 0xA>(v); // row_bcast:15 -> rows 1, 3
-    v = dpp_add<0x143, 0xC>(v); // row_bcast:31 -> rows 2, 3
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
 // ---------------------------------------------------------------------------------------------------------------
 // EMBEDDING (src/shaders/vkllm_embedding.comp:138-167) for contiguous rows
 __global__ void embed_rows_kernel(const uint32_t *toks, const uint16_t *embd, uint16_t *h, uint32_t V, uint32_t D,
@@ -761,397 +716,6 @@ __device__ void attn_row(const uint16_t *q, const uint16_t *K, const uint16_t *V
             s += part[k * dn + d];
         out[d0 + d] = f2h(s);
     }
-}
-
-// ---------------------------------------------------------------------------------------------------------------
-// Decode attention. The reference materialises fp16 scores, fp16 probabilities and an fp16 attention output
-// (src/models/vkllm_llama2_layers.c:223-257, src/shaders/vkllm_softmax.comp:42-96), so the probabilities are rounded
-// with the GLOBAL max and sum of the row. Two kernels keep those rounding points without any cross-block merge:
-//   attn_scores_kernel  split over the cache positions: chunk c of head h writes s_j = fp16(scale q.k_j) to the
-//                       scores scratch and its chunk max m_c and l_c = sum_j exp(s_j - m_c)
-//   attn_pv_kernel      split over the output dims: block (h, g) reduces M = max m_c, L = sum_c l_c exp(m_c - M)
-//                       (the same reduction in every block of the head), then p_j = fp16(exp(s_j - M) / L) and
-//                       out[d] = fp16(sum_j p_j v_j[d]) for its hd / G dims over all positions
-// The chunk length (a multiple of 16 positions) follows kv on the device, so one captured graph serves every
-// position. kv == hd takes the reference's transposed product p . V^T.
-
-__device__ __forceinline__ void attn_chunks(uint32_t kv, uint32_t hd, uint32_t cmax, uint32_t &ch, uint32_t &nc)
-{
-    if (kv == hd)
-    {
-        ch = kv;
-        nc = 1;
-        return;
-    }
-    ch = (kv + cmax - 1) / cmax;
-    ch = (ch + 15) / 16 * 16;
-    nc = (kv + ch - 1) / ch;
-}
-
-// Lanes sharing one cache row when scoring keys: each lane takes two 16-byte vectors (16 dims) of the row.
-__device__ __forceinline__ uint32_t key_lanes(uint32_t hd)
-{
-    uint32_t l = 1;
-    while (l * 16 < hd)
-        l <<= 1;
-    return l;
-}
-
-// sum over aligned groups of `lpk` lanes (1, 2, 4, 8 or 16) with in-row DPP; every lane gets its group's sum
-__device__ __forceinline__ float group_sum(float v, uint32_t lpk)
-{
-    if (lpk >= 2)
-        v = dpp_add<0xB1, 0xF>(v); // quad_perm [1,0,3,2]
-    if (lpk >= 4)
-        v = dpp_add<0x4E, 0xF>(v); // quad_perm [2,3,0,1]
-    if (lpk >= 8)
-        v = dpp_add<0x141, 0xF>(v); // row_half_mirror
-    if (lpk >= 16)
-        v = dpp_add<0x140, 0xF>(v); // row_mirror
-    return v;
-}
-
-template <int ctrl, int row_mask> __device__ __forceinline__ float dpp_max(float v)
-{
-    return fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), ctrl, row_mask,
-                                                               0xF, false)));
-}
-__device__ __forceinline__ float wave_max_dpp(float v)
-{
-    v = dpp_max<0xB1, 0xF>(v);
-    v = dpp_max<0x4E, 0xF>(v);
-    v = dpp_max<0x141, 0xF>(v);
-    v = dpp_max<0x140, 0xF>(v);
-    v = dpp_max<0x142, 0xA>(v);
-    v = dpp_max<0x143, 0xC>(v);
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
-// reductions over the 4 waves of a 256-thread block; `red` holds 4 floats and is not reused by the other one
-__device__ __forceinline__ float block4_max(float v, float *red)
-{
-    v = wave_max_dpp(v);
-    if ((threadIdx.x & 63) == 0)
-        red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-}
-__device__ __forceinline__ float block4_sum(float v, float *red)
-{
-    v = wave_sum_dpp(v);
-    if ((threadIdx.x & 63) == 0)
-        red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    return (red[0] + red[1]) + (red[2] + red[3]);
-}
-
-// sm[j] = fp16(scale * q . K[j]) for j < n (K: n contiguous rows of hd halfs); all 256 threads take part. A key is
-// scored by key_lanes(hd) lanes holding 16 dims each, U passes of keys in flight per thread, loads unconditional
-// at clamped addresses. The lanes of one key share their loop trip count, so the group DPP sees only live lanes.
-template <int U>
-__device__ __forceinline__ void attn_score_keys(const uint16_t *q, const uint16_t *K, uint32_t n, uint32_t hd,
-                                                float scale, float *sm)
-{
-    const uint32_t vpr = hd / 8, lpk = key_lanes(hd);
-    const uint32_t tid = threadIdx.x, kl = tid % lpk, ks = tid / lpk, kpp = 256 / lpk;
-    const uint32_t c0 = min(2 * kl, vpr - 1), c1 = min(2 * kl + 1, vpr - 1);
-    const u32x4 *qv = (const u32x4 *)q;
-    u32x4 q0 = qv[c0], q1 = qv[c1];
-    if (2 * kl >= vpr)
-        q0 = (u32x4){0, 0, 0, 0};
-    if (2 * kl + 1 >= vpr)
-        q1 = (u32x4){0, 0, 0, 0};
-    const u32x4 *Kv = (const u32x4 *)K;
-    for (uint32_t jb = ks; jb < n; jb += kpp * U)
-    {
-        u32x4 ka[U], kb[U];
-#pragma unroll
-        for (int t = 0; t < U; ++t)
-        {
-            const size_t row = (size_t)min(jb + kpp * t, n - 1) * vpr;
-            ka[t] = Kv[row + c0];
-            kb[t] = Kv[row + c1];
-        }
-#pragma unroll
-        for (int t = 0; t < U; ++t)
-        {
-            float p = dot8(kb[t], q1, dot8(ka[t], q0, 0.f));
-            p = group_sum(p, lpk);
-            const uint32_t j = jb + kpp * t;
-            if (kl == 0 && j < n)
-                sm[j] = h2f(f2h(p * scale));
-        }
-    }
-}
-
-__global__ __launch_bounds__(256) void attn_scores_kernel(AttnDecodeArgs a)
-{
-    extern __shared__ float sm[]; // this chunk's scores
-    __shared__ float rmax[4], rsum[4];
-    const uint32_t h = blockIdx.x / a.cmax, c = blockIdx.x % a.cmax;
-    const uint32_t kv = a.step->offset + 1;
-    uint32_t ch, nc;
-    attn_chunks(kv, a.hd, a.cmax, ch, nc);
-    if (c >= nc)
-        return;
-    const uint32_t tid = threadIdx.x;
-    const uint32_t j0 = c * ch, n = min(ch, kv - j0);
-    // chunks hold a few dozen positions: two passes of keys per thread cover them
-    attn_score_keys<2>(a.q + (size_t)h * a.hd, a.kc + ((size_t)h * a.ctx + j0) * a.hd, n, a.hd, a.scale, sm);
-    __syncthreads();
-    float mx = -FLT_MAX;
-    for (uint32_t j = tid; j < n; j += 256)
-        mx = fmaxf(mx, sm[j]);
-    mx = block4_max(mx, rmax);
-    float sum = 0.f;
-    for (uint32_t j = tid; j < n; j += 256)
-    {
-        sum += expf(sm[j] - mx);
-        a.scores[(size_t)h * a.ctx + j0 + j] = sm[j];
-    }
-    sum = block4_sum(sum, rsum);
-    if (tid == 0)
-    {
-        a.stats[((size_t)h * a.cmax + c) * 2] = mx;
-        a.stats[((size_t)h * a.cmax + c) * 2 + 1] = sum;
-    }
-}
-
-// out[r] = fp16(sum_k p_k V[r][k]) for the block's rows r of the reference's transposed product (kv == hd)
-__device__ __forceinline__ void attn_pv_transposed(const float *pl, const uint16_t *Vh, uint16_t *out, uint32_t kv,
-                                                   uint32_t hd, uint32_t d0, uint32_t dg)
-{
-    for (uint32_t r = threadIdx.x; r < dg; r += 256)
-    {
-        const uint16_t *row = Vh + (size_t)(d0 + r) * hd;
-        float acc = 0.f;
-        for (uint32_t k = 0; k < kv; ++k)
-            acc = fmaf(pl[k], h2f(row[k]), acc);
-        out[r] = f2h(acc);
-    }
-}
-
-// block b -> (head, dim group): the G blocks of a head get consecutive ids with equal b % 8, i.e. one XCD and its
-// L2, so the partial lines of V rows that neighbouring groups read are fetched from HBM once
-__device__ __forceinline__ void attn_block_head(uint32_t b, uint32_t G, uint32_t &h, uint32_t &g)
-{
-    h = (b % 8) + 8 * (b / (8 * G));
-    g = (b / 8) % G;
-}
-
-__global__ __launch_bounds__(256) void attn_pv_kernel(AttnDecodeArgs a)
-{
-    __shared__ float rmax[4], rsum[4];
-    __shared__ float part[2048];
-    uint32_t h, g;
-    attn_block_head(blockIdx.x, a.groups, h, g);
-    if (h >= a.H)
-        return;
-    const uint32_t tid = threadIdx.x;
-    const uint32_t kv = a.step->offset + 1;
-    uint32_t ch, nc;
-    attn_chunks(kv, a.hd, a.cmax, ch, nc);
-    const float *st = a.stats + (size_t)h * a.cmax * 2;
-    const float *S = a.scores + (size_t)h * a.ctx;
-    const uint16_t *Vh = a.vc + (size_t)h * a.ctx * a.hd;
-    const uint32_t dg = a.hd / a.groups, d0 = g * dg;
-    uint16_t *out = a.out + (size_t)h * a.hd + d0;
-    // loads in this order: chunk statistics, then V rows and scores, so waiting for the statistics (counters
-    // retire in issue order) does not wait for V
-    const uint32_t ci = min(tid, nc - 1);
-    const float mc_raw = st[2 * ci], lc_raw = st[2 * ci + 1];
-    const uint32_t lpr = dg / 8, vpr = a.hd / 8, rpp = 256 / lpr;
-    const uint32_t kl = tid % lpr, ks = tid / lpr;
-    const u32x4 *Vv = (const u32x4 *)Vh + d0 / 8 + kl;
-    constexpr int U = 8;
-    u32x4 vv[U];
-    float sc[U];
-#pragma unroll
-    for (int t = 0; t < U; ++t)
-    {
-        const uint32_t j = min(ks + rpp * t, kv - 1);
-        vv[t] = Vv[(size_t)j * vpr];
-        sc[t] = S[j];
-    }
-    // softmax statistics of the whole row, reduced identically by every block of the head
-    const float mc = tid < nc ? mc_raw : -FLT_MAX;
-    const float M = block4_max(mc, rmax);
-    const float L = block4_sum(tid < nc ? lc_raw * expf(mc - M) : 0.f, rsum);
-    if (kv == a.hd)
-    {
-        float *pl = part;
-        for (uint32_t j = tid; j < kv; j += 256)
-            pl[j] = h2f(f2h(expf(S[j] - M) / L));
-        __syncthreads();
-        attn_pv_transposed(pl, Vh, out, kv, a.hd, d0, dg);
-        return;
-    }
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (uint32_t jb = ks; jb < kv; jb += rpp * U)
-    {
-        if (jb != ks)
-        {
-#pragma unroll
-            for (int t = 0; t < U; ++t)
-            {
-                const uint32_t j = min(jb + rpp * t, kv - 1);
-                vv[t] = Vv[(size_t)j * vpr];
-                sc[t] = S[j];
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < U; ++t)
-        {
-            const float pj = jb + rpp * t < kv ? h2f(f2h(expf(sc[t] - M) / L)) : 0.f;
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-            {
-                acc[2 * e] = fmaf(pj, half_lo(vv[t][e]), acc[2 * e]);
-                acc[2 * e + 1] = fmaf(pj, half_hi(vv[t][e]), acc[2 * e + 1]);
-            }
-        }
-    }
-    if (ks < rpp)
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-            part[ks * dg + kl * 8 + e] = acc[e]; // rpp * dg <= 256 * 8
-    __syncthreads();
-    if (tid < dg)
-    {
-        float o = 0.f;
-        for (uint32_t k = 0; k < rpp; ++k)
-            o += part[k * dg + tid];
-        out[tid] = f2h(o);
-    }
-}
-
-// Short-context decode attention in one kernel: block (h, g) (the pv kernel's mapping) scores all kv keys of head h
-// itself, reduces the softmax statistics within the block and forms the probability-weighted sum for its dim
-// group. The G blocks of a head read the head's keys from one XCD's L2, so HBM sees them once; at long contexts
-// that re-reading costs more than the two-kernel path, which the host switches to. LDS: kv floats.
-__global__ __launch_bounds__(256) void attn_decode_small_kernel(AttnDecodeArgs a)
-{
-    extern __shared__ float sm[];
-    __shared__ float rmax[4], rsum[4];
-    __shared__ float part[2048];
-    uint32_t h, g;
-    attn_block_head(blockIdx.x, a.groups, h, g);
-    if (h >= a.H)
-        return;
-    const uint32_t tid = threadIdx.x;
-    const uint32_t kv = a.step->offset + 1;
-    const uint16_t *Vh = a.vc + (size_t)h * a.ctx * a.hd;
-    const uint32_t dg = a.hd / a.groups, d0 = g * dg;
-    const uint32_t lpr = dg / 8, vpr = a.hd / 8, rpp = 256 / lpr;
-    const uint32_t kl = tid % lpr, ks = tid / lpr;
-    // this block's first V rows, in flight while the scores are computed
-    constexpr int U = 8;
-    const u32x4 *Vv = (const u32x4 *)Vh + d0 / 8 + kl;
-    u32x4 vv[U];
-#pragma unroll
-    for (int t = 0; t < U; ++t)
-        vv[t] = Vv[(size_t)min(ks + rpp * t, kv - 1) * vpr];
-    attn_score_keys<16>(a.q + (size_t)h * a.hd, a.kc + (size_t)h * a.ctx * a.hd, kv, a.hd, a.scale, sm);
-    __syncthreads();
-    float mx = -FLT_MAX;
-    for (uint32_t j = tid; j < kv; j += 256)
-        mx = fmaxf(mx, sm[j]);
-    const float M = block4_max(mx, rmax);
-    float sum = 0.f;
-    for (uint32_t j = tid; j < kv; j += 256)
-        sum += expf(sm[j] - M);
-    const float L = block4_sum(sum, rsum);
-    for (uint32_t j = tid; j < kv; j += 256)
-        sm[j] = h2f(f2h(expf(sm[j] - M) / L));
-    __syncthreads();
-    uint16_t *out = a.out + (size_t)h * a.hd + d0;
-    if (kv == a.hd)
-    {
-        attn_pv_transposed(sm, Vh, out, kv, a.hd, d0, dg);
-        return;
-    }
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (uint32_t jb = ks; jb < kv; jb += rpp * U)
-    {
-        if (jb != ks)
-        {
-#pragma unroll
-            for (int t = 0; t < U; ++t)
-                vv[t] = Vv[(size_t)min(jb + rpp * t, kv - 1) * vpr];
-        }
-#pragma unroll
-        for (int t = 0; t < U; ++t)
-        {
-            const uint32_t j = jb + rpp * t;
-            const float pj = j < kv ? sm[min(j, kv - 1)] : 0.f;
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-            {
-                acc[2 * e] = fmaf(pj, half_lo(vv[t][e]), acc[2 * e]);
-                acc[2 * e + 1] = fmaf(pj, half_hi(vv[t][e]), acc[2 * e + 1]);
-            }
-        }
-    }
-    if (ks < rpp)
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-            part[ks * dg + kl * 8 + e] = acc[e];
-    __syncthreads();
-    if (tid < dg)
-    {
-        float o = 0.f;
-        for (uint32_t k = 0; k < rpp; ++k)
-            o += part[k * dg + tid];
-        out[tid] = f2h(o);
-    }
-}
-
-hipError_t launch_attn_small(hipStream_t st, const AttnDecodeArgs &a, uint32_t kv_max)
-{
-    if (a.hd % 8 != 0 || a.hd > 256 || a.H == 0 || a.groups == 0 || (a.hd / 8) % a.groups != 0 || kv_max == 0)
-        return hipErrorInvalidValue;
-    const uint32_t blocks = (a.H + 7) / 8 * 8 * a.groups;
-    attn_decode_small_kernel<<<blocks, 256, (size_t)kv_max * sizeof(float), st>>>(a);
-    return hipGetLastError();
-}
-
-static size_t attn_scores_lds(uint32_t hd, uint32_t ctx, uint32_t cmax)
-{
-    uint32_t ch = (ctx + cmax - 1) / cmax;
-    ch = (ch + 15) / 16 * 16;
-    return (size_t)(ch > hd ? ch : hd) * sizeof(float);
-}
-
-uint32_t attn_pv_groups(uint32_t H, uint32_t hd)
-{
-    // the largest divisor of the row's 16-byte vectors that is <= 8 while H * G stays <= 512 workgroups
-    uint32_t best = 1;
-    for (uint32_t g = 1; g <= 8; ++g)
-        if ((hd / 8) % g == 0 && H * g <= 512)
-            best = g;
-    return best;
-}
-
-static bool attn_decode_ok(const AttnDecodeArgs &a)
-{
-    return a.hd % 8 == 0 && a.hd <= 256 && a.cmax > 0 && a.H > 0 && a.groups > 0 && (a.hd / 8) % a.groups == 0;
-}
-
-hipError_t launch_attn_scores(hipStream_t st, const AttnDecodeArgs &a)
-{
-    if (!attn_decode_ok(a))
-        return hipErrorInvalidValue;
-    attn_scores_kernel<<<a.H * a.cmax, 256, attn_scores_lds(a.hd, a.ctx, a.cmax), st>>>(a);
-    return hipGetLastError();
-}
-
-hipError_t launch_attn_pv(hipStream_t st, const AttnDecodeArgs &a)
-{
-    if (!attn_decode_ok(a))
-        return hipErrorInvalidValue;
-    const uint32_t blocks = (a.H + 7) / 8 * 8 * a.groups;
-    attn_pv_kernel<<<blocks, 256, 0, st>>>(a);
-    return hipGetLastError();
 }
 
 // prefill: one workgroup per (query row, head); the transposition rule applies when the step's kv == hd

@@ -95,10 +95,11 @@ struct GemvArgs
 };
 hipError_t launch_gemv(hipStream_t st, int epi, const GemvArgs &a, int cu_count);
 
-// single-token attention over the cache for every head (kv = step->offset + 1): s_j = fp16(scale q.k_j),
+// Single-token attention over the cache for every head (kv = step->offset + 1): s_j = fp16(scale q.k_j),
 // p = fp16(softmax(s)), out[h*hd + d] = fp16(sum_j p_j v_j[d]); when kv == hd the product is p . V^T (the
-// reference's shape-based transposition rule). Scores are split into at most `cmax` chunks per head (multiples of
-// 16 positions); the probability-weighted sum into `groups` slices of the head's dims (attn_pv_groups).
+// reference's shape-based transposition rule). Long caches: attn_scores splits the keys into `cmax` chunks of
+// `chunk` positions (chunk * cmax >= ctx), attn_pv forms each chunk's partial sums and merges them.
+// Short caches: attn_small does it all in one kernel (`groups` slices of the head's dims, each scoring all keys).
 struct AttnDecodeArgs
 {
     const uint16_t *q;        // [H, hd]
@@ -107,14 +108,16 @@ struct AttnDecodeArgs
     const Step *step;
     float *scores;            // [H, ctx]
     float *stats;             // [H, cmax, 2]: chunk max, chunk sum of exp
-    uint32_t H, hd, ctx, cmax, groups;
+    float *part;              // [H, cmax, hd]: chunk partial sums
+    uint32_t *count;          // [H]: chunk arrivals, zero before the first launch; the kernels leave it zero
+    uint32_t H, hd, ctx, cmax, chunk, groups;
     float scale;
 };
-uint32_t attn_pv_groups(uint32_t H, uint32_t hd);
+// dim slices per head: the largest divisor of hd / 8 up to max_groups with H * groups <= 1024
+uint32_t attn_groups(uint32_t H, uint32_t hd, uint32_t max_groups);
 hipError_t launch_attn_scores(hipStream_t st, const AttnDecodeArgs &a);
 hipError_t launch_attn_pv(hipStream_t st, const AttnDecodeArgs &a);
-// the same attention in one kernel that recomputes a head's scores in each of its `groups` blocks (no scores or
-// statistics scratch); for kv <= kv_max, which sizes its LDS
+// kv <= kv_max <= ctx; kv_max sizes the LDS
 hipError_t launch_attn_small(hipStream_t st, const AttnDecodeArgs &a, uint32_t kv_max);
 
 // prefill: queries s < S at positions offset+s attend to positions <= offset+s
