@@ -40,6 +40,7 @@ struct FusedState
     // decode attention scratch: scores [H, ctx], chunk statistics [H, cmax, 2], chunk partial sums [H, cmax, hd]
     float *att_scores = nullptr, *att_stats = nullptr, *att_part = nullptr;
     uint32_t *att_count = nullptr; // per-head chunk arrivals of the merge, zero between launches
+    float *gemm_work = nullptr;    // split-K partial tiles of short-prompt prefill GEMMs
     uint32_t att_cmax = 0, att_chunk = 0;
     // decode attention in one kernel up to this many positions, in two kernels beyond (VKLLM_ATTN_SMALL_MAX)
     uint32_t attn_small_max = 0;
@@ -51,6 +52,9 @@ struct FusedState
     bool trace = false;
     uint64_t trace_steps = 0, trace_enqueue_ns = 0, trace_wait_ns = 0;
 };
+
+// split-K workspace of the prefill GEMMs: 16 MB, enough for 8 splits of a 128 x 4096 tile set
+static constexpr size_t kGemmWorkElems = (size_t)4 << 20;
 
 static uint64_t host_ns()
 {
@@ -116,7 +120,7 @@ void fused_model_release(vkllm_context *ctx, vkllm_models_llama2 *model)
         (void)hipFree(fs->step);
     if (fs->freqs)
         (void)hipFree(fs->freqs);
-    void *att[] = {fs->att_scores, fs->att_stats, fs->att_part, fs->att_count};
+    void *att[] = {fs->att_scores, fs->att_stats, fs->att_part, fs->att_count, fs->gemm_work};
     for (void *b : att)
         if (b)
             (void)hipFree(b);
@@ -160,6 +164,7 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         HIP_TRY(hipMalloc(&fs->att_part, H * C * mp->hd * sizeof(float)));
         HIP_TRY(hipMalloc(&fs->att_count, H * sizeof(uint32_t)));
         HIP_TRY(hipMemset(fs->att_count, 0, H * sizeof(uint32_t)));
+        HIP_TRY(hipMalloc(&fs->gemm_work, kGemmWorkElems * sizeof(float)));
     }
     FusedState *fs = mp->fs;
     if (S <= fs->cap_S)
@@ -328,20 +333,20 @@ static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S
     {
         const ModelPriv::Layer &ly = mp->layers[l];
         KTRY(ctx, KID_F_RMSNORM, vk::launch_rmsnorm_rows(st, fs->h, ly.attn_norm, fs->xn, S, D, mp->eps));
-        KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_PLAIN, fs->xn, ly.wqkv, fs->qkv, S, 3 * D, D, 3 * D, 0, cu));
+        KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_PLAIN, fs->xn, ly.wqkv, fs->qkv, S, 3 * D, D, 3 * D, 0, cu, fs->gemm_work, kGemmWorkElems));
         KTRY(ctx, KID_F_ROPE_KV,
              vk::launch_rope_kv(st, fs->qkv, fs->q, ly.kc, ly.vc, fs->freqs, offset, S, D, hd, mp->ctx));
         KTRY(ctx, KID_F_ATTN_PREFILL,
              vk::launch_attn_prefill(st, fs->q, ly.kc, ly.vc, fs->attn, offset, S, mp->H, hd, mp->ctx, scale));
-        KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_RESID, fs->attn, ly.wo, fs->h, S, D, D, D, 0, cu));
+        KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_RESID, fs->attn, ly.wo, fs->h, S, D, D, D, 0, cu, fs->gemm_work, kGemmWorkElems));
         KTRY(ctx, KID_F_RMSNORM, vk::launch_rmsnorm_rows(st, fs->h, ly.ffn_norm, fs->xn, S, D, mp->eps));
         KTRY(ctx, KID_F_GEMM,
-             vk::launch_gemm(st, vk::GEMM_SILU_HI, fs->xn, ly.wug, fs->ug, S, 2 * F, D, 2 * F, F, cu));
+             vk::launch_gemm(st, vk::GEMM_SILU_HI, fs->xn, ly.wug, fs->ug, S, 2 * F, D, 2 * F, F, cu, fs->gemm_work, kGemmWorkElems));
         KTRY(ctx, KID_F_SWIGLU, vk::launch_swiglu(st, fs->ug, fs->act, S, F));
-        KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_RESID, fs->act, ly.wd, fs->h, S, D, F, D, 0, cu));
+        KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_RESID, fs->act, ly.wd, fs->h, S, D, F, D, 0, cu, fs->gemm_work, kGemmWorkElems));
     }
     KTRY(ctx, KID_F_RMSNORM, vk::launch_rmsnorm_rows(st, fs->h, mp->out_norm, fs->xn, S, D, mp->eps));
-    KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_PLAIN, fs->xn, mp->out_w, fs->logits, S, V, D, V, 0, cu));
+    KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_PLAIN, fs->xn, mp->out_w, fs->logits, S, V, D, V, 0, cu, fs->gemm_work, kGemmWorkElems));
     KTRY(ctx, KID_F_ARGMAX, vk::launch_argmax_rows(st, fs->logits, fs->ids, S, V));
     return VKLLM_ERR_OK;
 }

@@ -520,9 +520,11 @@ template <int EPI, int R, int NV> static hipError_t launch_fast(hipStream_t st, 
         per_cu = n > 0 ? n : 1;
         cached_lds = lds;
     }
-    uint32_t blocks = (units + 3) / 4;
+    // every wave gets the same number of units (the fewest that the resident waves can cover), so no wave runs an
+    // extra unit while the others idle
     const uint32_t cap = (uint32_t)(cu_count > 0 ? cu_count : 256) * (uint32_t)per_cu;
-    blocks = blocks > cap ? cap : blocks;
+    const uint32_t per_wave = (units + 4 * cap - 1) / (4 * cap);
+    const uint32_t blocks = (units + 4 * per_wave - 1) / (4 * per_wave);
     gemv_fast_kernel<EPI, R, NV><<<blocks, 256, lds, st>>>(a, units);
     return hipGetLastError();
 }

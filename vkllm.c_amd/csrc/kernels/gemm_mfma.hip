@@ -1,12 +1,17 @@
 // Prefill GEMM on CDNA4 matrix cores: C[M, N] = A[M, K] . B[N, K]^T with fp16 operands and fp32 accumulation
-// (v_mfma_f32_16x16x32_f16), the dense replacement for src/shaders/vkllm_matmul_t1.comp on the token step's
-// weight products.
+// (v_mfma_f32_16x16x32_f16). It replaces src/shaders/vkllm_matmul_t1.comp for the token step's weight products,
+// where A holds the step's activations (M = tokens) and B a weight matrix stored [out, in].
 //
-// Tiling: BM x BN output tile per 256-thread workgroup (2 x 2 waves, each (BM/2) x (BN/2) as 16x16 MFMA blocks),
-// K in steps of 32. Tiles of A and B go through LDS with rows padded to 80 bytes, which keeps the 16-lane
-// ds_read_b128 operand fetches on distinct banks; the next K step's global loads are issued before the current
-// step's MFMAs. Tiles are ordered M-fastest and dealt to XCDs in contiguous runs so a run shares its B tiles in
-// one L2.
+// Tiling: a BM x BN output tile per 256-thread workgroup, 2 x 2 waves of (BM/2) x (BN/2) as 16x16 MFMA blocks,
+// K in steps of 64. Tiles of A and B go through two LDS buffers whose rows are padded to 144 bytes (the 16-lane
+// ds_read_b128 operand fetches then fall on distinct banks): while the MFMAs consume one buffer, the next K step's
+// global loads are in flight and land in the other, so each K step costs one barrier. Global loads are
+// unconditional at clamped addresses (a guarded load compiles to a branch and a wait per load).
+//
+// Short prompts (M <= 128) are bound by streaming B from HBM: one tile covers all of M so every weight is read
+// once, and narrow products split K over several workgroups so that enough of them stream at once; the fp32
+// partial tiles are then added in split order by gemm_splitk_reduce_kernel, which applies the epilogue.
+// Tiles are ordered M-fastest and dealt to XCDs in contiguous runs so a run shares its B tiles in one L2.
 #include "device_common.h"
 #include "kernels.h"
 
@@ -15,26 +20,44 @@ namespace vk
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4g __attribute__((ext_vector_type(4)));
 
-constexpr int kBK = 32;
-constexpr int kLdsRow = kBK + 8; // halfs per LDS row (80 bytes)
+constexpr int kBK = 64;
+constexpr int kLdsRow = kBK + 8; // halfs per LDS row (144 bytes)
 
-template <int BM, int BN, int EPI>
-__global__ __launch_bounds__(256) void gemm_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
-                                                   uint16_t *C, uint32_t M, uint32_t N, uint32_t K, uint32_t ldc,
-                                                   uint32_t split, uint32_t tiles_m, uint32_t tiles_total)
+__device__ __forceinline__ void gemm_store(int epi, uint16_t *C, uint32_t ldc, uint32_t m, uint32_t n, float v,
+                                           uint32_t split)
 {
-    constexpr int TM = BM / 32, TN = BN / 32; // 16x16 blocks per wave
-    constexpr int AV = BM * 4 / 256, BV = BN * 4 / 256; // 16-byte vectors per thread per K step
-    __shared__ __attribute__((aligned(16))) uint16_t As[BM * kLdsRow];
-    __shared__ __attribute__((aligned(16))) uint16_t Bs[BN * kLdsRow];
+    uint16_t *c = C + (size_t)m * ldc + n;
+    if (epi == GEMM_PLAIN)
+        *c = f2h(v);
+    else if (epi == GEMM_SILU_HI)
+        *c = f2h(n >= split ? silu(v) : v);
+    else
+        *c = f2h(h2f(*c) + h2f(f2h(v)));
+}
+
+// SPLIT: workgroup z of gridDim.y covers K columns [z * kchunk, min(K, (z + 1) * kchunk)) and writes its fp32 tile
+// to work[z][M][N] instead of C
+template <int BM, int BN, int EPI, bool SPLIT>
+__global__ __launch_bounds__(256) void gemm_kernel(const uint16_t *__restrict__ A, const uint16_t *__restrict__ B,
+                                                   uint16_t *C, float *work, uint32_t M, uint32_t N, uint32_t K,
+                                                   uint32_t ldc, uint32_t split, uint32_t kchunk, uint32_t tiles_m,
+                                                   uint32_t tiles_total)
+{
+    constexpr int TM = BM / 32, TN = BN / 32;            // 16x16 blocks per wave
+    constexpr int AV = BM * kBK / 8 / 256, BV = BN * kBK / 8 / 256; // 16-byte vectors per thread per K step
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+    // buffer b of A at lds[b BM rows], of B after both A buffers
+    auto As = [&](int b) { return lds + b * BM * kLdsRow; };
+    auto Bs = [&](int b) { return lds + 2 * BM * kLdsRow + b * BN * kLdsRow; };
 
     const uint32_t per_xcd = gridDim.x / 8;
     const uint32_t t = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
     if (t >= tiles_total)
         return;
     const uint32_t m0 = (t % tiles_m) * BM, n0 = (t / tiles_m) * BN;
+    const uint32_t kb = SPLIT ? blockIdx.y * kchunk : 0;
+    const uint32_t ke = SPLIT ? min(K, kb + kchunk) : K;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const uint32_t wm = wid >> 1, wn = wid & 1;
 
@@ -45,57 +68,70 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint16_t *__restrict__ 
         for (int j = 0; j < TN; ++j)
             acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-    u32x4g ra[AV], rb[BV];
-    // unconditional loads at clamped addresses (a guarded load compiles to a branch and a wait per load): rows
-    // past M or N only feed outputs that are not stored; K columns past the end are zeroed by a select
+    // rows past M or N only feed outputs that are never stored; columns past the K range are zeroed
+    u32x4 ra[AV], rb[BV];
     auto load = [&](uint32_t k0) {
 #pragma unroll
         for (int i = 0; i < AV; ++i)
         {
-            const uint32_t v = tid + 256 * i, row = min(m0 + v / 4, M - 1), kk = k0 + (v % 4) * 8;
-            const u32x4g x = *(const u32x4g *)(A + (size_t)row * K + min(kk, K - 8));
-            ra[i] = kk < K ? x : (u32x4g){0, 0, 0, 0};
+            const uint32_t v = tid + 256 * i, row = min(m0 + v / 8, M - 1), kk = k0 + (v % 8) * 8;
+            const u32x4 x = *(const u32x4 *)(A + (size_t)row * K + min(kk, K - 8));
+            ra[i] = kk < ke ? x : (u32x4){0, 0, 0, 0};
         }
 #pragma unroll
         for (int i = 0; i < BV; ++i)
         {
-            const uint32_t v = tid + 256 * i, row = min(n0 + v / 4, N - 1), kk = k0 + (v % 4) * 8;
-            const u32x4g x = *(const u32x4g *)(B + (size_t)row * K + min(kk, K - 8));
-            rb[i] = kk < K ? x : (u32x4g){0, 0, 0, 0};
+            const uint32_t v = tid + 256 * i, row = min(n0 + v / 8, N - 1), kk = k0 + (v % 8) * 8;
+            const u32x4 x = __builtin_nontemporal_load((const u32x4 *)(B + (size_t)row * K + min(kk, K - 8)));
+            rb[i] = kk < ke ? x : (u32x4){0, 0, 0, 0};
         }
     };
-
-    load(0);
-    for (uint32_t k0 = 0; k0 < K; k0 += kBK)
-    {
+    auto stash = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < AV; ++i)
         {
             const uint32_t v = tid + 256 * i;
-            *(u32x4g *)(As + (v / 4) * kLdsRow + (v % 4) * 8) = ra[i];
+            *(u32x4 *)(As(buf) + (v / 8) * kLdsRow + (v % 8) * 8) = ra[i];
         }
 #pragma unroll
         for (int i = 0; i < BV; ++i)
         {
             const uint32_t v = tid + 256 * i;
-            *(u32x4g *)(Bs + (v / 4) * kLdsRow + (v % 4) * 8) = rb[i];
+            *(u32x4 *)(Bs(buf) + (v / 8) * kLdsRow + (v % 8) * 8) = rb[i];
         }
-        __syncthreads();
-        if (k0 + kBK < K)
+    };
+
+    load(kb);
+    stash(0);
+    __syncthreads();
+    int cur = 0;
+    for (uint32_t k0 = kb; k0 < ke; k0 += kBK)
+    {
+        const bool more = k0 + kBK < ke;
+        if (more)
             load(k0 + kBK);
-        f16x8 af[TM], bf[TN];
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-            af[i] = *(const f16x8 *)(As + (wm * (BM / 2) + i * 16 + lane % 16) * kLdsRow + (lane / 16) * 8);
+        for (int kk = 0; kk < kBK; kk += 32)
+        {
+            f16x8 af[TM], bf[TN];
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-            bf[j] = *(const f16x8 *)(Bs + (wn * (BN / 2) + j * 16 + lane % 16) * kLdsRow + (lane / 16) * 8);
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
+            for (int i = 0; i < TM; ++i)
+                af[i] = *(const f16x8 *)(As(cur) + (wm * (BM / 2) + i * 16 + lane % 16) * kLdsRow + kk +
+                                         (lane / 16) * 8);
 #pragma unroll
             for (int j = 0; j < TN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                bf[j] = *(const f16x8 *)(Bs(cur) + (wn * (BN / 2) + j * 16 + lane % 16) * kLdsRow + kk +
+                                         (lane / 16) * 8);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (more)
+            stash(cur ^ 1);
         __syncthreads();
+        cur ^= 1;
     }
 
     // lane holds C[4*(lane/16) + e][lane % 16] of each 16x16 block
@@ -110,49 +146,289 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint16_t *__restrict__ 
                 const uint32_t n = n0 + wn * (BN / 2) + j * 16 + lane % 16;
                 if (m >= M || n >= N)
                     continue;
-                const float v = acc[i][j][e];
-                uint16_t *c = C + (size_t)m * ldc + n;
-                if (EPI == GEMM_PLAIN)
-                    *c = f2h(v);
-                else if (EPI == GEMM_SILU_HI)
-                    *c = f2h(n >= split ? silu(v) : v);
+                if (SPLIT)
+                    work[((size_t)blockIdx.y * M + m) * N + n] = acc[i][j][e];
                 else
-                    *c = f2h(h2f(*c) + h2f(f2h(v)));
+                    gemm_store(EPI, C, ldc, m, n, acc[i][j][e], split);
             }
 }
 
-template <int BM, int BN>
-static hipError_t launch_tile(hipStream_t st, int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, uint32_t M,
-                              uint32_t N, uint32_t K, uint32_t ldc, uint32_t split)
+// Weight-streaming GEMM for short prompts (M <= 16 MB): each of the 4 waves owns 32 rows of B (two 16-column MFMA
+// blocks) and all of M. B goes straight from HBM into registers, 32 contiguous bytes per lane (a lane's bytes feed
+// k slots 16 (lane / 16) + [0, 16) of a 64-column step, A's fragments use the same slots), one 128-column chunk
+// ahead of the MFMAs. A's chunk [16 MB, 128] is staged in a double-buffered LDS tile shared by the waves, so each
+// 128 columns cost one barrier. SPLIT as in gemm_kernel (chunks of kchunk columns, a multiple of 128).
+constexpr int kStreamKC = 128;                  // columns per chunk
+constexpr int kStreamLdsRow = kStreamKC + 8;    // halfs per LDS row (272 bytes)
+
+template <int EPI, bool SPLIT, int MB>
+__global__ __launch_bounds__(256) void gemm_stream_kernel(const uint16_t *__restrict__ A,
+                                                          const uint16_t *__restrict__ B, uint16_t *C, float *work,
+                                                          uint32_t M, uint32_t N, uint32_t K, uint32_t ldc,
+                                                          uint32_t split, uint32_t kchunk, uint32_t tiles_total)
 {
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+    auto As = [&](int b) { return lds + b * (MB * 16) * kStreamLdsRow; };
+    const uint32_t per_xcd = gridDim.x / 8;
+    const uint32_t t = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (t >= tiles_total)
+        return;
+    const uint32_t n0 = t * 128;
+    const uint32_t kb = SPLIT ? blockIdx.y * kchunk : 0;
+    const uint32_t ke = SPLIT ? min(K, kb + kchunk) : K;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const uint32_t ks = 16 * (lane / 16); // this lane's k slots within a 64-column step
+
+    f32x4 acc[MB][2];
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+        acc[i][0] = acc[i][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    // B: rows n0 + 32 wid + 16 j + lane % 16 (clamped: their outputs are never stored); columns past the K range
+    // are zeroed by a select after unconditional loads at clamped addresses
+    const uint16_t *brow[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+        brow[j] = B + (size_t)min(n0 + 32 * wid + 16 * j + lane % 16, N - 1) * K;
+    u32x4 bcur[2][2][2], bnext[2][2][2]; // [n block][64-column half][16-byte vector]
+    auto load_b = [&](uint32_t k0, u32x4 (&bb)[2][2][2]) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int v = 0; v < 2; ++v)
+                {
+                    const uint32_t kk = k0 + 64 * h + ks + 8 * v;
+                    const u32x4 x = __builtin_nontemporal_load((const u32x4 *)(brow[j] + min(kk, K - 8)));
+                    bb[j][h][v] = kk < ke ? x : (u32x4){0, 0, 0, 0};
+                }
+    };
+    // A: chunk rows 0..16 MB - 1 (clamped to M - 1), 16 vectors per row, MB vectors per thread
+    u32x4 ra[MB];
+    auto load_a = [&](uint32_t k0) {
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+        {
+            const uint32_t v = tid + 256 * i, row = min(v / 16, M - 1), kk = k0 + (v % 16) * 8;
+            const u32x4 x = *(const u32x4 *)(A + (size_t)row * K + min(kk, K - 8));
+            ra[i] = kk < ke ? x : (u32x4){0, 0, 0, 0};
+        }
+    };
+    auto stash_a = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+        {
+            const uint32_t v = tid + 256 * i;
+            *(u32x4 *)(As(buf) + (v / 16) * kStreamLdsRow + (v % 16) * 8) = ra[i];
+        }
+    };
+
+    load_a(kb);
+    load_b(kb, bcur);
+    stash_a(0);
+    __syncthreads();
+    int cur = 0;
+    for (uint32_t k0 = kb; k0 < ke; k0 += kStreamKC)
+    {
+        const bool more = k0 + kStreamKC < ke;
+        if (more)
+        {
+            load_b(k0 + kStreamKC, bnext);
+            load_a(k0 + kStreamKC);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int v = 0; v < 2; ++v)
+            {
+                f16x8 bf[2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    bf[j] = __builtin_bit_cast(f16x8, bcur[j][h][v]);
+#pragma unroll
+                for (int i = 0; i < MB; ++i)
+                {
+                    const f16x8 af = *(const f16x8 *)(As(cur) + (i * 16 + lane % 16) * kStreamLdsRow + 64 * h + ks +
+                                                      8 * v);
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
+                }
+            }
+        if (more)
+        {
+            stash_a(cur ^ 1);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int v = 0; v < 2; ++v)
+                        bcur[j][h][v] = bnext[j][h][v];
+        }
+        __syncthreads();
+        cur ^= 1;
+    }
+
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+            {
+                const uint32_t m = i * 16 + 4 * (lane / 16) + e;
+                const uint32_t n = n0 + 32 * wid + 16 * j + lane % 16;
+                if (m >= M || n >= N)
+                    continue;
+                if (SPLIT)
+                    work[((size_t)blockIdx.y * M + m) * N + n] = acc[i][j][e];
+                else
+                    gemm_store(EPI, C, ldc, m, n, acc[i][j][e], split);
+            }
+}
+
+// C = epilogue(sum over z of work[z]) for split-K products, the splits added in order
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float *work, uint16_t *C, uint32_t M,
+                                                                 uint32_t N, uint32_t ldc, uint32_t split,
+                                                                 uint32_t splits)
+{
+    const uint64_t total = (uint64_t)M * N;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (uint64_t)gridDim.x * 256)
+    {
+        float v = 0.f;
+        for (uint32_t z = 0; z < splits; ++z)
+            v += work[(size_t)z * total + i];
+        gemm_store(EPI, C, ldc, (uint32_t)(i / N), (uint32_t)(i % N), v, split);
+    }
+}
+
+template <int BM, int BN> static size_t gemm_lds()
+{
+    return (size_t)2 * (BM + BN) * kLdsRow * sizeof(uint16_t);
+}
+
+template <int BM, int BN, int EPI, bool SPLIT>
+static hipError_t launch_tile(hipStream_t st, const uint16_t *A, const uint16_t *B, uint16_t *C, float *work,
+                              uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, uint32_t splits,
+                              uint32_t kchunk)
+{
+    static bool attr_set = false; // LDS beyond the default 64 KB needs the attribute, once per kernel
+    const size_t lds = gemm_lds<BM, BN>();
+    if (!attr_set)
+    {
+        hipError_t e = hipFuncSetAttribute((const void *)gemm_kernel<BM, BN, EPI, SPLIT>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess)
+            return e;
+        attr_set = true;
+    }
     const uint32_t tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN, total = tm * tn;
     const uint32_t grid = (total + 7) / 8 * 8;
-    switch (epi)
-    {
-    case GEMM_PLAIN:
-        gemm_kernel<BM, BN, GEMM_PLAIN><<<grid, 256, 0, st>>>(A, B, C, M, N, K, ldc, split, tm, total);
-        break;
-    case GEMM_SILU_HI:
-        gemm_kernel<BM, BN, GEMM_SILU_HI><<<grid, 256, 0, st>>>(A, B, C, M, N, K, ldc, split, tm, total);
-        break;
-    case GEMM_RESID:
-        gemm_kernel<BM, BN, GEMM_RESID><<<grid, 256, 0, st>>>(A, B, C, M, N, K, ldc, split, tm, total);
-        break;
-    default:
-        return hipErrorInvalidValue;
-    }
+    gemm_kernel<BM, BN, EPI, SPLIT><<<dim3(grid, SPLIT ? splits : 1), 256, lds, st>>>(A, B, C, work, M, N, K, ldc,
+                                                                                     split, kchunk, tm, total);
     return hipGetLastError();
 }
 
-hipError_t launch_gemm(hipStream_t st, int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, uint32_t M,
-                       uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, int cu_count)
+template <int BM, int BN, int EPI>
+static hipError_t launch_shape(hipStream_t st, const uint16_t *A, const uint16_t *B, uint16_t *C, float *work,
+                               uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, uint32_t splits,
+                               uint32_t kchunk)
 {
-    if (K % 8 != 0 || M == 0 || N == 0)
+    if (splits <= 1)
+        return launch_tile<BM, BN, EPI, false>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
+    hipError_t e = launch_tile<BM, BN, EPI, true>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk);
+    if (e != hipSuccess)
+        return e;
+    const uint64_t total = (uint64_t)M * N;
+    uint32_t grid = (uint32_t)((total + 255) / 256);
+    grid = grid > 4096 ? 4096 : grid;
+    gemm_splitk_reduce_kernel<EPI><<<grid, 256, 0, st>>>(work, C, M, N, ldc, split, splits);
+    return hipGetLastError();
+}
+
+template <int EPI, int MB, bool SPLIT>
+static hipError_t launch_stream_tile(hipStream_t st, const uint16_t *A, const uint16_t *B, uint16_t *C, float *work,
+                                     uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split,
+                                     uint32_t splits, uint32_t kchunk)
+{
+    static bool attr_set = false;
+    const size_t lds = (size_t)2 * MB * 16 * kStreamLdsRow * sizeof(uint16_t);
+    if (!attr_set)
+    {
+        hipError_t e = hipFuncSetAttribute((const void *)gemm_stream_kernel<EPI, SPLIT, MB>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess)
+            return e;
+        attr_set = true;
+    }
+    const uint32_t tiles = (N + 127) / 128;
+    const uint32_t grid = (tiles + 7) / 8 * 8;
+    gemm_stream_kernel<EPI, SPLIT, MB><<<dim3(grid, SPLIT ? splits : 1), 256, lds, st>>>(A, B, C, work, M, N, K, ldc,
+                                                                                        split, kchunk, tiles);
+    return hipGetLastError();
+}
+
+template <int EPI, int MB>
+static hipError_t launch_stream(hipStream_t st, const uint16_t *A, const uint16_t *B, uint16_t *C, float *work,
+                                uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, uint32_t splits,
+                                uint32_t kchunk)
+{
+    if (splits <= 1)
+        return launch_stream_tile<EPI, MB, false>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
+    hipError_t e = launch_stream_tile<EPI, MB, true>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk);
+    if (e != hipSuccess)
+        return e;
+    const uint64_t total = (uint64_t)M * N;
+    uint32_t grid = (uint32_t)((total + 255) / 256);
+    grid = grid > 4096 ? 4096 : grid;
+    gemm_splitk_reduce_kernel<EPI><<<grid, 256, 0, st>>>(work, C, M, N, ldc, split, splits);
+    return hipGetLastError();
+}
+
+template <int EPI>
+static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint16_t *B, uint16_t *C, float *work,
+                                  size_t work_elems, uint32_t M, uint32_t N, uint32_t K, uint32_t ldc,
+                                  uint32_t split, int cu_count)
+{
+    const uint32_t cus = cu_count > 0 ? (uint32_t)cu_count : 256;
+    if (M <= 128)
+    {
+        // weight-streaming regime: a 128-row tile covers all of M so each weight is read once; K is split over
+        // workgroups when N is narrow
+        const uint32_t tiles = (N + 63) / 64;
+        uint32_t splits = 1;
+        while (tiles * splits <= cus && K / (splits * 2) >= 512 && (size_t)splits * 2 * M * N <= work_elems)
+            splits *= 2;
+        const uint32_t kchunk = ((K + splits - 1) / splits + kBK - 1) / kBK * kBK;
+        splits = (K + kchunk - 1) / kchunk;
+        return launch_shape<128, 64, EPI>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk);
+    }
+    const uint64_t big = (uint64_t)((M + 127) / 128) * ((N + 127) / 128);
+    if (big >= cus)
+        return launch_shape<128, 128, EPI>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
+    return launch_shape<128, 64, EPI>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
+}
+
+hipError_t launch_gemm(hipStream_t st, int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, uint32_t M,
+                       uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, int cu_count, float *work,
+                       size_t work_elems)
+{
+    if (K % 8 != 0 || K < 8 || M == 0 || N == 0)
         return hipErrorInvalidValue;
-    const uint64_t big_tiles = (uint64_t)((M + 127) / 128) * ((N + 127) / 128);
-    if (big_tiles >= (uint64_t)(cu_count > 0 ? cu_count : 256))
-        return launch_tile<128, 128>(st, epi, A, B, C, M, N, K, ldc, split);
-    return launch_tile<64, 64>(st, epi, A, B, C, M, N, K, ldc, split);
+    switch (epi)
+    {
+    case GEMM_PLAIN:
+        return launch_epi_gemm<GEMM_PLAIN>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count);
+    case GEMM_SILU_HI:
+        return launch_epi_gemm<GEMM_SILU_HI>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count);
+    case GEMM_RESID:
+        return launch_epi_gemm<GEMM_RESID>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count);
+    default:
+        return hipErrorInvalidValue;
+    }
 }
 
 } // namespace vk

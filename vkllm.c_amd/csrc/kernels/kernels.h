@@ -141,8 +141,10 @@ enum GemmEpi : int
     GEMM_RESID = 2,   // C = fp16(C + fp16(acc)) (C holds the residual)
 };
 // C[M, N] (row stride ldc) = A[M, K] . B[N, K]^T, fp16 operands, fp32 accumulation on MFMA. K % 8 == 0.
+// `work` (work_elems floats) holds split-K partial tiles for short prompts; with too little of it K is not split.
 hipError_t launch_gemm(hipStream_t st, int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, uint32_t M,
-                       uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, int cu_count);
+                       uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, int cu_count, float *work,
+                       size_t work_elems);
 
 // ---- synthetic weights: dst[i] = fp16(normal(stream, i) * std), i < count ----
 hipError_t launch_random_f16(hipStream_t st, uint16_t *dst, uint64_t count, uint64_t stream_key, float std);

@@ -708,6 +708,20 @@ extern "C" vkllm_err_t vkllm_models_llama2_free(struct vkllm_context *context, s
 // =============================================================================================================
 // graph construction: src/models/vkllm_llama2_layers.c:13-354, src/models/vkllm_models_llama2.c:488-602
 
+// dst = a + "." + b (truncated to n - 1 bytes): node names are built for every node of every step, and a formatted
+// print per name costs more than the rest of building the node
+static void scope_name(char *dst, size_t n, const char *a, const char *b)
+{
+    const size_t la = strnlen(a, n - 1);
+    memcpy(dst, a, la);
+    size_t at = la;
+    if (at < n - 1)
+        dst[at++] = '.';
+    const size_t lb = strnlen(b, n - 1 - at);
+    memcpy(dst + at, b, lb);
+    dst[at + lb] = '\0';
+}
+
 extern "C" vkllm_err_t vkllm_llama2_build_ffn_layer(struct vkllm_context *context, struct vkllm_graph *graph,
                                                     struct vkllm_tensor *input,
                                                     struct vkllm_llama2_ffn_layer_params params, uint32_t block_idx)
@@ -721,7 +735,7 @@ extern "C" vkllm_err_t vkllm_llama2_build_ffn_layer(struct vkllm_context *contex
 
     vkllm_tensor *norm_srcs[] = {input, params.norm_weight};
     vkllm_op_rmsnorm_params np = {params.norm_power, params.norm_eps};
-    snprintf(scope, sizeof(scope), "%s.norm", name);
+    scope_name(scope, sizeof(scope), name, "norm");
     _CHECK(vkllm_tensor_new(context, scope, input->shapes, input->dtype, VKLLM_OP_RMSNORM, norm_srcs, 2, &np,
                             sizeof(np), false, &t));
     vkllm_tensor *norm = t;
@@ -731,7 +745,7 @@ extern "C" vkllm_err_t vkllm_llama2_build_ffn_layer(struct vkllm_context *contex
     uint32_t up_shapes[4] = {batch, channel, seq, up_dim};
     vkllm_op_matmul_params mp0 = {1.0f, 0}, mp1 = {1.0f, 1};
     vkllm_tensor *up_srcs[] = {norm, params.WU};
-    snprintf(scope, sizeof(scope), "%s.up", name);
+    scope_name(scope, sizeof(scope), name, "up");
     _CHECK(vkllm_tensor_new(context, scope, up_shapes, norm->dtype, VKLLM_OP_MATMUL, up_srcs, 2, &mp0, sizeof(mp0),
                             false, &t));
     vkllm_tensor *up = t;
@@ -739,7 +753,7 @@ extern "C" vkllm_err_t vkllm_llama2_build_ffn_layer(struct vkllm_context *contex
         return vkllm_tensor_free(context, up), VKLLM_ERR_ALLOC;
 
     vkllm_tensor *gate_srcs[] = {norm, params.WG};
-    snprintf(scope, sizeof(scope), "%s.gate", name);
+    scope_name(scope, sizeof(scope), name, "gate");
     _CHECK(vkllm_tensor_new(context, scope, up_shapes, norm->dtype, VKLLM_OP_MATMUL, gate_srcs, 2, &mp1, sizeof(mp1),
                             false, &t));
     vkllm_tensor *gate = t;
@@ -748,7 +762,7 @@ extern "C" vkllm_err_t vkllm_llama2_build_ffn_layer(struct vkllm_context *contex
 
     int32_t mul_op = 2;
     vkllm_tensor *mul_srcs[] = {up, gate};
-    snprintf(scope, sizeof(scope), "%s.mul", name);
+    scope_name(scope, sizeof(scope), name, "mul");
     _CHECK(vkllm_tensor_new(context, scope, up_shapes, gate->dtype, VKLLM_OP_BIN, mul_srcs, 2, &mul_op,
                             sizeof(mul_op), false, &t));
     vkllm_tensor *gate_mul = t;
@@ -757,7 +771,7 @@ extern "C" vkllm_err_t vkllm_llama2_build_ffn_layer(struct vkllm_context *contex
 
     uint32_t down_shapes[4] = {batch, channel, seq, params.WD->shapes[2]};
     vkllm_tensor *down_srcs[] = {gate_mul, params.WD};
-    snprintf(scope, sizeof(scope), "%s.down", name);
+    scope_name(scope, sizeof(scope), name, "down");
     _CHECK(vkllm_tensor_new(context, scope, down_shapes, gate_mul->dtype, VKLLM_OP_MATMUL, down_srcs, 2, &mp0,
                             sizeof(mp0), false, &t));
     vkllm_tensor *down = t;
@@ -766,7 +780,7 @@ extern "C" vkllm_err_t vkllm_llama2_build_ffn_layer(struct vkllm_context *contex
 
     int32_t add_op = 0;
     vkllm_tensor *add_srcs[] = {input, down};
-    snprintf(scope, sizeof(scope), "%s.add", name);
+    scope_name(scope, sizeof(scope), name, "add");
     _CHECK(vkllm_tensor_new(context, scope, input->shapes, input->dtype, VKLLM_OP_BIN, add_srcs, 2, &add_op,
                             sizeof(add_op), false, &t));
     if (vkllm_graph_add_node(context, graph, t) != VKLLM_ERR_OK)
@@ -807,7 +821,7 @@ extern "C" vkllm_err_t vkllm_llama2_build_self_attn_layer(struct vkllm_context *
 
     vkllm_tensor *norm_srcs[] = {input, params.norm_weight};
     vkllm_op_rmsnorm_params np = {params.norm_power, params.norm_eps};
-    snprintf(scope, sizeof(scope), "%s.norm", name);
+    scope_name(scope, sizeof(scope), name, "norm");
     _CHECK(vkllm_tensor_new(context, scope, input->shapes, input->dtype, VKLLM_OP_RMSNORM, norm_srcs, 2, &np,
                             sizeof(np), false, &t));
     vkllm_tensor *norm = t;
@@ -821,7 +835,7 @@ extern "C" vkllm_err_t vkllm_llama2_build_self_attn_layer(struct vkllm_context *
     for (int i = 0; i < 3; ++i)
     {
         vkllm_tensor *srcs[] = {norm, W[i]};
-        snprintf(scope, sizeof(scope), "%s.%s", name, pn[i]);
+        scope_name(scope, sizeof(scope), name, pn[i]);
         _CHECK(vkllm_tensor_new(context, scope, qkv_shapes, norm->dtype, VKLLM_OP_MATMUL, srcs, 2, &mm, sizeof(mm),
                                 false, &t));
         proj[i] = t;
@@ -846,12 +860,12 @@ extern "C" vkllm_err_t vkllm_llama2_build_self_attn_layer(struct vkllm_context *
     }
     vkllm_tensor *Q_ref = refs[0], *K_ref = refs[1], *V_ref = refs[2];
 
-    snprintf(scope, sizeof(scope), "%s.RQ", name);
+    scope_name(scope, sizeof(scope), name, "RQ");
     _CHECK(vkllm_tensor_new(context, scope, Q_ref->shapes, Q_ref->dtype, VKLLM_OP_ROPE, &Q_ref, 1, &rope,
                             sizeof(rope), false, &t));
     vkllm_tensor *RQ = t;
     ADD_OR_FREE(RQ);
-    snprintf(scope, sizeof(scope), "%s.RK", name);
+    scope_name(scope, sizeof(scope), name, "RK");
     _CHECK(vkllm_tensor_new(context, scope, K_ref->shapes, K_ref->dtype, VKLLM_OP_ROPE, &K_ref, 1, &rope,
                             sizeof(rope), false, &t));
     vkllm_tensor *RK = t;
@@ -864,14 +878,14 @@ extern "C" vkllm_err_t vkllm_llama2_build_self_attn_layer(struct vkllm_context *
     uint32_t scores_shapes[4] = {batch, params.num_head, seq, key_num};
     vkllm_op_matmul_params smm = {1.0f / sqrtf((float)hd), 0};
     vkllm_tensor *scores_srcs[] = {RQ, RK};
-    snprintf(scope, sizeof(scope), "%s.scores", name);
+    scope_name(scope, sizeof(scope), name, "scores");
     _CHECK(vkllm_tensor_new(context, scope, scores_shapes, input->dtype, VKLLM_OP_MATMUL, scores_srcs, 2, &smm,
                             sizeof(smm), false, &t));
     vkllm_tensor *scores = t;
     ADD_OR_FREE(scores);
 
     vkllm_op_softmax_params sp = {1, rope.offset};
-    snprintf(scope, sizeof(scope), "%s.attn_weights", name);
+    scope_name(scope, sizeof(scope), name, "attn_weights");
     _CHECK(vkllm_tensor_new(context, scope, scores_shapes, input->dtype, VKLLM_OP_SOFTMAX, &scores, 1, &sp,
                             sizeof(sp), false, &t));
     vkllm_tensor *attn_w = t;
@@ -893,7 +907,7 @@ extern "C" vkllm_err_t vkllm_llama2_build_self_attn_layer(struct vkllm_context *
     }
     ADD_OR_FREE(output_ref);
 
-    snprintf(scope, sizeof(scope), "%s.concated_heads", name);
+    scope_name(scope, sizeof(scope), name, "concated_heads");
     _CHECK(vkllm_tensor_new(context, scope, output_ref->shapes, output_ref->dtype, VKLLM_OP_COPY, &output_ref, 1,
                             nullptr, 0, false, &t));
     vkllm_tensor *concat = t;
@@ -907,7 +921,7 @@ extern "C" vkllm_err_t vkllm_llama2_build_self_attn_layer(struct vkllm_context *
     uint32_t fo_shapes[4] = {batch, 1, seq, hidden};
     vkllm_tensor *fo_srcs[] = {concat_ref, params.WO};
     vkllm_op_matmul_params om = {1.0f, 0};
-    snprintf(scope, sizeof(scope), "%s.final_output", name);
+    scope_name(scope, sizeof(scope), name, "final_output");
     _CHECK(vkllm_tensor_new(context, scope, fo_shapes, concat->dtype, VKLLM_OP_MATMUL, fo_srcs, 2, &om, sizeof(om),
                             false, &t));
     vkllm_tensor *fo = t;
@@ -915,7 +929,7 @@ extern "C" vkllm_err_t vkllm_llama2_build_self_attn_layer(struct vkllm_context *
 
     int32_t add_op = 0;
     vkllm_tensor *add_srcs[] = {input, fo};
-    snprintf(scope, sizeof(scope), "%s.final_output_add", name);
+    scope_name(scope, sizeof(scope), name, "final_output_add");
     _CHECK(vkllm_tensor_new(context, scope, fo->shapes, fo->dtype, VKLLM_OP_BIN, add_srcs, 2, &add_op, sizeof(add_op),
                             false, &t));
     ADD_OR_FREE(t);

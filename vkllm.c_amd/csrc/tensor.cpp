@@ -6,6 +6,16 @@
 
 #include "runtime.h"
 
+// dst = src + suffix, truncated to n - 1 bytes (views are made for every node of every step; no formatted print)
+static void name_with_suffix(char *dst, size_t n, const char *src, const char *suffix)
+{
+    const size_t ls = strnlen(src, n - 1);
+    memcpy(dst, src, ls);
+    const size_t lx = strnlen(suffix, n - 1 - ls);
+    memcpy(dst + ls, suffix, lx);
+    dst[ls + lx] = '\0';
+}
+
 // contiguous byte strides, W innermost (src/core/vkllm_tensor.c:13-31)
 static void calc_strides(const uint32_t *shapes, vkllm_dtype_t dtype, uint32_t *strides)
 {
@@ -81,7 +91,8 @@ extern "C" vkllm_err_t vkllm_tensor_new(struct vkllm_context *context, const cha
     auto *t = (vkllm_tensor *)calloc(1, sizeof(vkllm_tensor) + params_bytes);
     if (!t)
         return VKLLM_ERR_ALLOC;
-    snprintf((char *)t->name, sizeof(t->name), "%s", name ? name : "");
+    if (name)
+        memcpy((char *)t->name, name, strnlen(name, sizeof(t->name) - 1)); // calloc left the terminator
     t->dtype = dtype;
     memcpy(t->shapes, shapes, sizeof(t->shapes));
     calc_strides(shapes, dtype, t->strides);
@@ -210,7 +221,7 @@ extern "C" vkllm_err_t vkllm_tensor_copy_ref(struct vkllm_context *context, stru
     auto *t = (vkllm_tensor *)calloc(1, sizeof(vkllm_tensor));
     if (!t)
         return VKLLM_ERR_ALLOC;
-    snprintf((char *)t->name, sizeof(t->name), "%s_ref", tensor->name);
+    name_with_suffix((char *)t->name, sizeof(t->name), tensor->name, "_ref");
     t->dtype = tensor->dtype;
     memcpy(t->shapes, tensor->shapes, sizeof(t->shapes));
     memcpy(t->strides, tensor->strides, sizeof(t->strides));
@@ -235,7 +246,7 @@ extern "C" vkllm_err_t vkllm_tensor_slice0(struct vkllm_context *context, struct
         _CHECK_ARGS(extents[i] <= tensor->shapes[i] && extents[i] > 0);
     _CHECK(vkllm_tensor_copy_ref(context, tensor, slice));
     vkllm_tensor *t = *slice;
-    snprintf((char *)t->name, sizeof(t->name), "%s_slice0", tensor->name);
+    name_with_suffix((char *)t->name, sizeof(t->name), tensor->name, "_slice0");
     memcpy(t->shapes, extents, sizeof(t->shapes));
     return VKLLM_ERR_OK;
 }
