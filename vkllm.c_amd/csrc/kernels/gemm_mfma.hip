@@ -8,9 +8,9 @@
 // global loads are in flight and land in the other, so each K step costs one barrier. Global loads are
 // unconditional at clamped addresses (a guarded load compiles to a branch and a wait per load).
 //
-// Short prompts (M <= 128) are bound by streaming B from HBM: one tile covers all of M so every weight is read
-// once, and narrow products split K over several workgroups so that enough of them stream at once; the fp32
-// partial tiles are then added in split order by gemm_splitk_reduce_kernel, which applies the epilogue.
+// Short prompts (M <= 128): one tile covers all of M so every weight is read once, and narrow products split K
+// over several workgroups so that enough of them run at once; the fp32 partial tiles are then added in split
+// order by gemm_splitk_reduce_kernel, which applies the epilogue.
 // Tiles are ordered M-fastest and dealt to XCDs in contiguous runs so a run shares its B tiles in one L2.
 #include "device_common.h"
 #include "kernels.h"
@@ -153,142 +153,6 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint16_t *__restrict__ 
             }
 }
 
-// Weight-streaming GEMM for short prompts (M <= 16 MB): each of the 4 waves owns 32 rows of B (two 16-column MFMA
-// blocks) and all of M. B goes straight from HBM into registers, 32 contiguous bytes per lane (a lane's bytes feed
-// k slots 16 (lane / 16) + [0, 16) of a 64-column step, A's fragments use the same slots), one 128-column chunk
-// ahead of the MFMAs. A's chunk [16 MB, 128] is staged in a double-buffered LDS tile shared by the waves, so each
-// 128 columns cost one barrier. SPLIT as in gemm_kernel (chunks of kchunk columns, a multiple of 128).
-constexpr int kStreamKC = 128;                  // columns per chunk
-constexpr int kStreamLdsRow = kStreamKC + 8;    // halfs per LDS row (272 bytes)
-
-template <int EPI, bool SPLIT, int MB>
-__global__ __launch_bounds__(256) void gemm_stream_kernel(const uint16_t *__restrict__ A,
-                                                          const uint16_t *__restrict__ B, uint16_t *C, float *work,
-                                                          uint32_t M, uint32_t N, uint32_t K, uint32_t ldc,
-                                                          uint32_t split, uint32_t kchunk, uint32_t tiles_total)
-{
-    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-    auto As = [&](int b) { return lds + b * (MB * 16) * kStreamLdsRow; };
-    const uint32_t per_xcd = gridDim.x / 8;
-    const uint32_t t = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-    if (t >= tiles_total)
-        return;
-    const uint32_t n0 = t * 128;
-    const uint32_t kb = SPLIT ? blockIdx.y * kchunk : 0;
-    const uint32_t ke = SPLIT ? min(K, kb + kchunk) : K;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-    const uint32_t ks = 16 * (lane / 16); // this lane's k slots within a 64-column step
-
-    f32x4 acc[MB][2];
-#pragma unroll
-    for (int i = 0; i < MB; ++i)
-        acc[i][0] = acc[i][1] = (f32x4){0.f, 0.f, 0.f, 0.f};
-
-    // B: rows n0 + 32 wid + 16 j + lane % 16 (clamped: their outputs are never stored); columns past the K range
-    // are zeroed by a select after unconditional loads at clamped addresses
-    const uint16_t *brow[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-        brow[j] = B + (size_t)min(n0 + 32 * wid + 16 * j + lane % 16, N - 1) * K;
-    u32x4 bcur[2][2][2], bnext[2][2][2]; // [n block][64-column half][16-byte vector]
-    auto load_b = [&](uint32_t k0, u32x4 (&bb)[2][2][2]) {
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int v = 0; v < 2; ++v)
-                {
-                    const uint32_t kk = k0 + 64 * h + ks + 8 * v;
-                    const u32x4 x = __builtin_nontemporal_load((const u32x4 *)(brow[j] + min(kk, K - 8)));
-                    bb[j][h][v] = kk < ke ? x : (u32x4){0, 0, 0, 0};
-                }
-    };
-    // A: chunk rows 0..16 MB - 1 (clamped to M - 1), 16 vectors per row, MB vectors per thread
-    u32x4 ra[MB];
-    auto load_a = [&](uint32_t k0) {
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-        {
-            const uint32_t v = tid + 256 * i, row = min(v / 16, M - 1), kk = k0 + (v % 16) * 8;
-            const u32x4 x = *(const u32x4 *)(A + (size_t)row * K + min(kk, K - 8));
-            ra[i] = kk < ke ? x : (u32x4){0, 0, 0, 0};
-        }
-    };
-    auto stash_a = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-        {
-            const uint32_t v = tid + 256 * i;
-            *(u32x4 *)(As(buf) + (v / 16) * kStreamLdsRow + (v % 16) * 8) = ra[i];
-        }
-    };
-
-    load_a(kb);
-    load_b(kb, bcur);
-    stash_a(0);
-    __syncthreads();
-    int cur = 0;
-    for (uint32_t k0 = kb; k0 < ke; k0 += kStreamKC)
-    {
-        const bool more = k0 + kStreamKC < ke;
-        if (more)
-        {
-            load_b(k0 + kStreamKC, bnext);
-            load_a(k0 + kStreamKC);
-        }
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int v = 0; v < 2; ++v)
-            {
-                f16x8 bf[2];
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    bf[j] = __builtin_bit_cast(f16x8, bcur[j][h][v]);
-#pragma unroll
-                for (int i = 0; i < MB; ++i)
-                {
-                    const f16x8 af = *(const f16x8 *)(As(cur) + (i * 16 + lane % 16) * kStreamLdsRow + 64 * h + ks +
-                                                      8 * v);
-#pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[j], acc[i][j], 0, 0, 0);
-                }
-            }
-        if (more)
-        {
-            stash_a(cur ^ 1);
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int h = 0; h < 2; ++h)
-#pragma unroll
-                    for (int v = 0; v < 2; ++v)
-                        bcur[j][h][v] = bnext[j][h][v];
-        }
-        __syncthreads();
-        cur ^= 1;
-    }
-
-#pragma unroll
-    for (int i = 0; i < MB; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-            {
-                const uint32_t m = i * 16 + 4 * (lane / 16) + e;
-                const uint32_t n = n0 + 32 * wid + 16 * j + lane % 16;
-                if (m >= M || n >= N)
-                    continue;
-                if (SPLIT)
-                    work[((size_t)blockIdx.y * M + m) * N + n] = acc[i][j][e];
-                else
-                    gemm_store(EPI, C, ldc, m, n, acc[i][j][e], split);
-            }
-}
-
 // C = epilogue(sum over z of work[z]) for split-K products, the splits added in order
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float *work, uint16_t *C, uint32_t M,
@@ -340,45 +204,6 @@ static hipError_t launch_shape(hipStream_t st, const uint16_t *A, const uint16_t
     if (splits <= 1)
         return launch_tile<BM, BN, EPI, false>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
     hipError_t e = launch_tile<BM, BN, EPI, true>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk);
-    if (e != hipSuccess)
-        return e;
-    const uint64_t total = (uint64_t)M * N;
-    uint32_t grid = (uint32_t)((total + 255) / 256);
-    grid = grid > 4096 ? 4096 : grid;
-    gemm_splitk_reduce_kernel<EPI><<<grid, 256, 0, st>>>(work, C, M, N, ldc, split, splits);
-    return hipGetLastError();
-}
-
-template <int EPI, int MB, bool SPLIT>
-static hipError_t launch_stream_tile(hipStream_t st, const uint16_t *A, const uint16_t *B, uint16_t *C, float *work,
-                                     uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split,
-                                     uint32_t splits, uint32_t kchunk)
-{
-    static bool attr_set = false;
-    const size_t lds = (size_t)2 * MB * 16 * kStreamLdsRow * sizeof(uint16_t);
-    if (!attr_set)
-    {
-        hipError_t e = hipFuncSetAttribute((const void *)gemm_stream_kernel<EPI, SPLIT, MB>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess)
-            return e;
-        attr_set = true;
-    }
-    const uint32_t tiles = (N + 127) / 128;
-    const uint32_t grid = (tiles + 7) / 8 * 8;
-    gemm_stream_kernel<EPI, SPLIT, MB><<<dim3(grid, SPLIT ? splits : 1), 256, lds, st>>>(A, B, C, work, M, N, K, ldc,
-                                                                                        split, kchunk, tiles);
-    return hipGetLastError();
-}
-
-template <int EPI, int MB>
-static hipError_t launch_stream(hipStream_t st, const uint16_t *A, const uint16_t *B, uint16_t *C, float *work,
-                                uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, uint32_t splits,
-                                uint32_t kchunk)
-{
-    if (splits <= 1)
-        return launch_stream_tile<EPI, MB, false>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
-    hipError_t e = launch_stream_tile<EPI, MB, true>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk);
     if (e != hipSuccess)
         return e;
     const uint64_t total = (uint64_t)M * N;
