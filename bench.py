@@ -1,25 +1,29 @@
 #!/usr/bin/env python3
 """Throughput of the vkllm LLaMA-2 token loop on one MI355X.
 
-Workload: LLaMA-2-7B-shaped decoder (dim 4096, 32 layers, 32 heads of 128, FFN 11008, vocab 32000), fp16
-weights generated on the device from seed 0 (weights N(0, 0.02), norm weights 1.0), a 128-token uniform-random
-prompt (seed 1) prefilled, then greedy decode at batch 1. Every token goes through the library's C API exactly
-as the reference's driver loop does (tests/vkllm_test_infer_gguf.c:183-270): tensor_new(input, mapped) ->
-graph_new -> models_llama2_build_graph -> graph_init -> upload -> graph_run -> graph_post_run ->
-tensor_invalid_cache -> read the arg-max id -> graph_free.
-
+Workloads (--config; the default is the headline one):
+  7b       LLaMA-2-7B-shaped decoder (dim 4096, 32 layers, 32 heads of 128, FFN 11008, vocab 32000), a 128-token
+           uniform-random prompt prefilled, then greedy decode at batch 1 in a 4096-position KV cache
+  7b-long  the same model, a 1024-token prompt, then 3072 greedy steps (tok/s also reported near positions 1k, 2k
+           and 4k, where attention over the cache grows from 4% to 13% of the bytes)
+  13b      LLaMA-2-13B-shaped decoder (dim 5120, 40 layers, 40 heads of 128, FFN 13824, vocab 32000), a 2048-token
+           prompt, then 128 greedy steps
+fp16 weights are generated on the device from seed 0 (N(0, 0.02), norm weights 1.0); prompt ids from seed 1.
+Every token goes through the library's C API exactly as the reference's driver loop does
+(tests/vkllm_test_infer_gguf.c:181-272): tensor_new(input, mapped) -> graph_new -> models_llama2_build_graph ->
+graph_init -> upload -> graph_run -> graph_post_run -> tensor_invalid_cache -> read the arg-max id -> graph_free.
 The loop runs in C (vkllm_hip_token_loop, the same API calls), so no interpreter sits between tokens.
 
 Printed (one JSON line on stdout):
-  value        decode tokens/s over exactly `--steps` timed single-token steps of that loop (host work included,
+  value        decode tokens/s over exactly the timed single-token steps of that loop (host work included,
                weights and KV cache resident in HBM)
   graph_replay_tok_s  the same decode step as back-to-back replays of its captured hipGraph (device time only)
   kernels      each decode kernel's average duration over back-to-back launches between one hipEvent pair on the
                library's stream, and its algorithmic GB/s
   roofline     the dominant decode kernel (the fused RMSNorm + gate/up GEMV + SwiGLU): algorithmic bytes per
-               launch / its average duration over 128 back-to-back launches across the 32 layers' weights
+               launch / its average duration over back-to-back launches across all layers' weights
   cpu_baseline the C oracle (scalar, double accumulation) timing a decode step of a 2-layer slice of the same
-               shape, scaled to 32 layers by multiply-accumulate count
+               shape, scaled to the full depth by multiply-accumulate count
 """
 import argparse
 import json
@@ -33,11 +37,20 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(HERE, "vkllm.c_amd"))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
-
-SHAPE = dict(n_layer=32, dim=4096, n_head=32, ffn=11008, vocab=32000)
-PROMPT_LEN = 128
-ATTN_SMALL_MAX = 1536  # positions up to which the decode attention is one kernel (VKLLM_ATTN_SMALL_MAX)
 MODEL_SEED, PROMPT_SEED = 0, 1
+ATTN_SMALL_MAX = 1536  # positions up to which the decode attention is one kernel (VKLLM_ATTN_SMALL_MAX)
+
+SHAPE_7B = dict(n_layer=32, dim=4096, n_head=32, ffn=11008, vocab=32000)
+SHAPE_13B = dict(n_layer=40, dim=5120, n_head=40, ffn=13824, vocab=32000)
+CONFIGS = {
+    "7b": dict(shape=SHAPE_7B, prompt=128, steps=256, warmup=8, ctx=4096, name="LLaMA-2-7B-shaped decoder (dim 4096, "
+               "32 layers, 32 heads, FFN 11008, vocab 32000), 128-token prompt prefill then greedy decode at batch 1"),
+    "7b-long": dict(shape=SHAPE_7B, prompt=1024, steps=3071, warmup=0, ctx=4096, name="LLaMA-2-7B-shaped decoder, "
+                    "4096-position KV cache, 1024-token prompt prefill then 3072 greedy steps at batch 1"),
+    "13b": dict(shape=SHAPE_13B, prompt=2048, steps=127, warmup=0, ctx=2304, name="LLaMA-2-13B-shaped decoder "
+                "(dim 5120, 40 layers, 40 heads, FFN 13824, vocab 32000), 2048-token prompt prefill then 128 greedy "
+                "steps at batch 1"),
+}
 
 
 def log(*a):
@@ -47,25 +60,33 @@ def log(*a):
 def decode_bytes(shape, kv):
     """Algorithmic HBM bytes of each fused decode kernel for one token at `kv` cached positions (fp16 weights
     and activations, fp32 norm weights). Each weight is read once; activations and cache rows as written."""
-    D, F, V, L = shape["dim"], shape["ffn"], shape["vocab"], shape["n_layer"]
+    D, F, V = shape["dim"], shape["ffn"], shape["vocab"]
+    attn = 2 * kv * D * 2 + D * 2 + D * 2
     return {
         "fused_embed": D * 2 * 2,
         "fused_qkv_rope": 3 * D * D * 2 + D * 2 + D * 4 + D * 2 + 2 * D * 2,
-        "fused_attn_scores": 2 * kv * D * 2 + D * 2 + D * 2,
-        "fused_attn_small": 2 * kv * D * 2 + D * 2 + D * 2,
+        "fused_attn_small": attn,
+        "fused_attn_scores": attn,
         "fused_o_resid": D * D * 2 + D * 2 + 2 * D * 2,
         "fused_gateup": 2 * F * D * 2 + D * 2 + D * 4 + F * 2,
         "fused_down_resid": D * F * 2 + F * 2 + 2 * D * 2,
         "fused_logits": V * D * 2 + D * 2 + D * 4 + V * 2,
         "fused_argmax": V * 2 + 4,
-        "_layers": L,
     }
 
 
-def read_traffic(kernel):
+def step_bytes(shape, kv):
+    """Whole decode step at `kv` positions: the per-layer kernels times the depth, plus embed, logits, arg max."""
+    b = decode_bytes(shape, kv)
+    per_layer = sum(b[k] for k in ("fused_qkv_rope", "fused_attn_scores", "fused_o_resid", "fused_gateup",
+                                   "fused_down_resid"))
+    return per_layer * shape["n_layer"] + b["fused_embed"] + b["fused_logits"] + b["fused_argmax"]
+
+
+def read_traffic(kernel, tag):
     """HBM bytes per launch of `kernel` measured with rocprofv3 FETCH_SIZE/WRITE_SIZE, from the committed
-    summary profiles/<kernel>_7b_pmc.txt (line 'traffic_bytes_per_launch: N'); None when absent."""
-    path = os.path.join(HERE, "profiles", f"{kernel}_7b_pmc.txt")
+    summary profiles/<kernel>_<tag>_pmc.txt (line 'traffic_bytes_per_launch: N'); None when absent."""
+    path = os.path.join(HERE, "profiles", f"{kernel}_{tag}_pmc.txt")
     try:
         with open(path) as f:
             for line in f:
@@ -79,8 +100,6 @@ def read_traffic(kernel):
 def copy_calibration(ctx, vk, mib):
     """Runs the library's COPY op (contiguous fp16, `mib` MiB read and written) 4 times: a kernel of known HBM
     traffic against which rocprofv3's FETCH_SIZE / WRITE_SIZE counters are scaled."""
-    import numpy as np
-
     n = mib * (1 << 20) // 2
     src = ctx.tensor_from(np.zeros(n, dtype=np.float16).reshape(1, 1, 1, n), name="calib_src")
     dst = ctx.tensor([1, 1, 1, n], vk.F16, "calib_dst", vk.OP_COPY, [src])
@@ -91,15 +110,15 @@ def copy_calibration(ctx, vk, mib):
     log(f"copy calibration: 4 copies of {mib} MiB")
 
 
-def cpu_baseline(seconds):
+def cpu_baseline(shape, seconds):
     """Decode tokens/s of the C oracle on one host core. The sample is decode steps of a 2-layer model of the
-    same widths (dim 4096, FFN 11008, vocab 32000) from an empty cache, timed until `seconds` have passed,
-    scaled to 32 layers by multiply-accumulate count (matmuls are > 99% of the oracle's work)."""
+    same widths from an empty cache, timed until `seconds` have passed, scaled to the full depth by
+    multiply-accumulate count (matmuls are > 99% of the oracle's work)."""
     sys.path.insert(0, os.path.join(HERE, "oracle"))
     import oracle_ffi as oracle
 
-    D, F, V = SHAPE["dim"], SHAPE["ffn"], SHAPE["vocab"]
-    cfg = oracle.make_cfg(2, D, SHAPE["n_head"], F, vocab=V, ctx=64)
+    D, F, V = shape["dim"], shape["ffn"], shape["vocab"]
+    cfg = oracle.make_cfg(2, D, shape["n_head"], F, vocab=V, ctx=64)
     m = oracle.Model(cfg=cfg, seed=MODEL_SEED)
     try:
         tok = [int(oracle.prompt_tokens(PROMPT_SEED, 1, V)[0])]
@@ -114,39 +133,47 @@ def cpu_baseline(seconds):
     finally:
         m.close()
     mac_layer = 4 * D * D + 3 * D * F
-    scale = (SHAPE["n_layer"] * mac_layer + V * D) / (2 * mac_layer + V * D)
+    scale = (shape["n_layer"] * mac_layer + V * D) / (2 * mac_layer + V * D)
     per_token = el / n * scale
     return {
         "value": round(1.0 / per_token, 5),
         "unit": "tok/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"{n} decode steps of a 2-layer dim-4096/FFN-11008/vocab-32000 slice in {el:.1f} s on one core, "
-                  f"x{scale:.2f} by MAC count to 32 layers",
+        "sample": f"{n} decode steps of a 2-layer dim-{D}/FFN-{F}/vocab-{V} slice in {el:.1f} s on one core, "
+                  f"x{scale:.2f} by MAC count to {shape['n_layer']} layers",
     }
 
 
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256, help="timed decode steps")
-    ap.add_argument("--warmup", type=int, default=8, help="untimed decode steps before the timed ones")
-    ap.add_argument("--prefill-reps", type=int, default=4, help="timed 128-token prefills")
+    ap.add_argument("--config", choices=sorted(CONFIGS), default="7b")
+    ap.add_argument("--steps", type=int, default=None, help="timed decode steps (default: the workload's)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed decode steps before the timed ones")
+    ap.add_argument("--prefill-reps", type=int, default=4, help="timed prompt prefills")
     ap.add_argument("--timing-steps", type=int, default=32, help="graph replays timed for the device-only rate")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample length (0: skip)")
-    ap.add_argument("--ctx", type=int, default=4096, help="KV cache positions")
+    ap.add_argument("--ctx", type=int, default=None, help="KV cache positions (default: the workload's)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first run the COPY op on MIB MiB (reference kernel for rocprofv3 byte counters)")
     args = ap.parse_args()
+    conf = CONFIGS[args.config]
+    shape = conf["shape"]
+    steps = conf["steps"] if args.steps is None else args.steps
+    warmup = conf["warmup"] if args.warmup is None else args.warmup
+    ctx_len = conf["ctx"] if args.ctx is None else args.ctx
+    prompt_len = conf["prompt"]
+    L = shape["n_layer"]
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py runs on one GPU: the token loop of this library is single-device (asked for "
               f"--gpus {args.gpus}, WORLD_SIZE {world})", file=sys.stderr)
         sys.exit(2)
-    need = PROMPT_LEN + args.warmup + args.steps + args.timing_steps + 1
-    if need > args.ctx:
-        sys.exit(f"--ctx {args.ctx} is smaller than the {need} positions the run uses")
+    need = prompt_len + warmup + steps + 1
+    if need > ctx_len:
+        sys.exit(f"--ctx {ctx_len} is smaller than the {need} positions the run uses")
 
     os.environ.setdefault("VKLLM_QUIET", "1")
     import pyvkllm as vk
@@ -154,34 +181,44 @@ def main():
     ctx = vk.Ctx(0)
     if args.copy_calibration > 0:
         copy_calibration(ctx, vk, args.copy_calibration)
-    log(f"device {ctx.arch()}; generating the 7B-shaped model on the device")
-    cfg = vk.llama_config(SHAPE["n_layer"], SHAPE["dim"], SHAPE["n_head"], SHAPE["ffn"], SHAPE["vocab"], args.ctx)
+    log(f"device {ctx.arch()}; generating the {args.config} model on the device")
+    cfg = vk.llama_config(L, shape["dim"], shape["n_head"], shape["ffn"], shape["vocab"], ctx_len)
     model = vk.Model(ctx, config=cfg, seed=MODEL_SEED)
-    prompt = vk.prompt_tokens(PROMPT_SEED, PROMPT_LEN, SHAPE["vocab"])
+    prompt = vk.prompt_tokens(PROMPT_SEED, prompt_len, shape["vocab"])
 
-    # prefill: one untimed, then timed repetitions of the same 128-token step at offset 0, each through the
-    # C token loop (one step: tensor_new, graph_new, build_graph, init, upload, run, post_run, free)
+    # prefill: one untimed, then timed repetitions of the same prompt step at offset 0, each through the C token
+    # loop (one step: tensor_new, graph_new, build_graph, init, upload, run, post_run, free)
     model.loop(prompt, 1)
     prefill_ns = []
     for _ in range(args.prefill_reps):
         _, sns, _ = model.loop(prompt, 1)
         prefill_ns.append(int(sns[0]))
     prefill_s = float(np.median(prefill_ns)) / 1e9
-    log(f"prefill {PROMPT_LEN} tokens: {prefill_s * 1e3:.2f} ms (median of {args.prefill_reps})")
+    log(f"prefill {prompt_len} tokens: {prefill_s * 1e3:.2f} ms (median of {args.prefill_reps})")
 
     # decode: prefill + warmup steps untimed, then exactly `steps` single-token steps in one C loop
-    ids, _, _ = model.loop(prompt, 1 + args.warmup)
-    pos = PROMPT_LEN + args.warmup
+    ids, _, _ = model.loop(prompt, 1 + warmup)
+    pos0 = prompt_len + warmup
     ctx.sync()
     t0 = time.perf_counter()
-    ids, step_ns, phase_ns = model.loop([int(ids[-1])], args.steps, offset=pos)
+    ids, step_ns, phase_ns = model.loop([int(ids[-1])], steps, offset=pos0)
     ctx.sync()
     decode_s = time.perf_counter() - t0
-    pos += args.steps
-    tps = args.steps / decode_s
-    host = {k: round(float(v) / max(args.steps - 1, 1) / 1e3, 2)
+    pos = pos0 + steps
+    tps = steps / decode_s
+    host = {k: round(float(v) / max(steps - 1, 1) / 1e3, 2)
             for k, v in zip(("build_us", "init_upload_us", "run_us", "free_us"), phase_ns)}
-    log(f"decode: {args.steps} steps in {decode_s:.3f} s = {tps:.1f} tok/s; per step {host}")
+    log(f"decode: {steps} steps in {decode_s:.3f} s = {tps:.1f} tok/s; per step {host}")
+    at_positions = {}
+    for target in (1024, 2048, 4096):
+        # the 64 timed steps ending at the target position (or starting there when it is the first one),
+        # from the per-step wall times
+        if steps < 64 or not pos0 <= target <= pos + 1:
+            continue
+        lo = min(max(0, target - pos0 - 64), steps - 64)
+        at_positions[str(target)] = round(64 / (float(np.sum(step_ns[lo:lo + 64])) / 1e9), 1)
+    if at_positions:
+        log(f"decode tok/s near positions: {at_positions}")
 
     # device time per token: replays of the captured decode graph, back to back, no host work in between
     # (not available when graph replay is switched off, e.g. VKLLM_GRAPH=0 under a kernel tracer)
@@ -191,20 +228,19 @@ def main():
         log(f"decode graph replay: {replay_ns / 1e3:.1f} us per token = {1e9 / replay_ns:.1f} tok/s")
 
     # per-kernel durations: back-to-back launches between one hipEvent pair on the library's stream
-    kv_mid = pos
-    nbytes = decode_bytes(SHAPE, kv_mid)
+    nbytes = decode_bytes(shape, pos)
     kernels = {}
     step_kernel_ns = 0.0
-    small_attn = kv_mid <= ATTN_SMALL_MAX  # the library's default switch-over to the two-kernel attention
+    small_attn = pos <= ATTN_SMALL_MAX  # the library's default switch-over to the two-kernel attention
     for name in ("fused_embed", "fused_qkv_rope", "fused_attn_small", "fused_attn_scores", "fused_attn_pv",
                  "fused_o_resid", "fused_gateup", "fused_down_resid", "fused_logits", "fused_argmax"):
         per_layer = name not in ("fused_embed", "fused_logits", "fused_argmax")
-        reps = 4 * SHAPE["n_layer"] if per_layer else 32
+        reps = 4 * L if per_layer else 32
         avg_ns = model.time_kernel(name, reps)
         used = not ((name == "fused_attn_small" and not small_attn) or
                     (name in ("fused_attn_scores", "fused_attn_pv") and small_attn))
         if used:
-            step_kernel_ns += avg_ns * (SHAPE["n_layer"] if per_layer else 1)
+            step_kernel_ns += avg_ns * (L if per_layer else 1)
         row = {"avg_us": round(avg_ns / 1e3, 3)}
         if name in nbytes:
             row["GBps"] = round(nbytes[name] / avg_ns, 1)
@@ -214,34 +250,29 @@ def main():
     dom_avg_ns = kernels[dom]["avg_us"] * 1e3
     achieved = nbytes[dom] / dom_avg_ns  # GB/s
     # bytes of the average timed step: the cache length at the middle of the timed steps
-    mean_bytes = decode_bytes(SHAPE, PROMPT_LEN + args.warmup + args.steps // 2 + 1)
-    step_bytes = sum(v for k, v in mean_bytes.items() if k in ("fused_qkv_rope", "fused_attn_scores", "fused_o_resid",
-                                                               "fused_gateup", "fused_down_resid")) * SHAPE["n_layer"]
-    step_bytes += mean_bytes["fused_embed"] + mean_bytes["fused_logits"] + mean_bytes["fused_argmax"]
-    traffic = read_traffic(dom)
+    mean_step_bytes = step_bytes(shape, pos0 + steps // 2 + 1)
+    traffic = read_traffic(dom, "7b") if shape is SHAPE_7B else None
 
     result = {
         "metric": "decode tok/s + % HBM roofline, LLaMA-2-7B-shape fp16 bs=1; prefill tok/s",
         "value": round(tps, 2),
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(decode_s / args.steps * 1e3, 4),
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(decode_s / steps * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16 storage, f32 accumulate",
         "data": "synthetic: device-generated random-init weights (seed 0), uniform-random prompt ids (seed 1)",
-        "config": {"workload": "LLaMA-2-7B-shaped decoder (dim 4096, 32 layers, 32 heads, FFN 11008, vocab 32000), "
-                               "128-token prompt prefill then greedy decode at batch 1",
-                   "prompt": PROMPT_LEN, "decode_positions": [PROMPT_LEN + args.warmup,
-                                                              PROMPT_LEN + args.warmup + args.steps],
-                   "kv_cache_positions": args.ctx},
-        "prefill_tok_s": round(PROMPT_LEN / prefill_s, 1),
+        "config": {"workload": conf["name"], "name": args.config, "prompt": prompt_len,
+                   "decode_positions": [pos0, pos], "kv_cache_positions": ctx_len},
+        "prefill_tok_s": round(prompt_len / prefill_s, 1),
         "prefill_ms": round(prefill_s * 1e3, 3),
-        "decode_hbm_roofline_frac": round(step_bytes / (decode_s / args.steps) / 1e9 / HBM_PEAK_GBS, 4),
-        "decode_bytes_per_token": step_bytes,
+        "decode_hbm_roofline_frac": round(mean_step_bytes / (decode_s / steps) / 1e9 / HBM_PEAK_GBS, 4),
+        "decode_bytes_per_token": mean_step_bytes,
+        "decode_tok_s_near_position": at_positions or None,
         "kernel_ms_per_step": round(step_kernel_ns / 1e6, 4),
         "graph_replay_ms_per_step": round(replay_ns / 1e6, 4) if replay_ns else None,
         "graph_replay_tok_s": round(1e9 / replay_ns, 1) if replay_ns else None,
@@ -255,7 +286,7 @@ def main():
     ctx.close()
     if args.cpu_seconds > 0:
         log("cpu baseline (oracle, one core)")
-        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(shape, args.cpu_seconds)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)
