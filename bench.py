@@ -68,6 +68,7 @@ def decode_bytes(shape, kv):
         "fused_attn_small": attn,
         "fused_attn_scores": attn,
         "fused_o_resid": D * D * 2 + D * 2 + 2 * D * 2,
+        "fused_attn_o": attn + D * D * 2 + 2 * D * 2,
         "fused_gateup": 2 * F * D * 2 + D * 2 + D * 4 + F * 2,
         "fused_down_resid": D * F * 2 + F * 2 + 2 * D * 2,
         "fused_logits": V * D * 2 + D * 2 + D * 4 + V * 2,
@@ -232,13 +233,20 @@ def main():
     kernels = {}
     step_kernel_ns = 0.0
     small_attn = pos <= ATTN_SMALL_MAX  # the library's default switch-over to the two-kernel attention
-    for name in ("fused_embed", "fused_qkv_rope", "fused_attn_small", "fused_attn_scores", "fused_attn_pv",
-                 "fused_o_resid", "fused_gateup", "fused_down_resid", "fused_logits", "fused_argmax"):
+    # short caches: attention and the output projection run as one launch with VKLLM_ATTN_O=1
+    attn_o = small_attn and os.environ.get("VKLLM_ATTN_O", "0") == "1"
+    for name in ("fused_embed", "fused_qkv_rope", "fused_attn_o", "fused_attn_small", "fused_attn_scores",
+                 "fused_attn_pv", "fused_o_resid", "fused_gateup", "fused_down_resid", "fused_logits", "fused_argmax"):
         per_layer = name not in ("fused_embed", "fused_logits", "fused_argmax")
         reps = 4 * L if per_layer else 32
+        if name in ("fused_attn_o", "fused_attn_small") and pos > ATTN_SMALL_MAX:
+            continue  # the one-kernel attention takes at most ATTN_SMALL_MAX positions
         avg_ns = model.time_kernel(name, reps)
-        used = not ((name == "fused_attn_small" and not small_attn) or
-                    (name in ("fused_attn_scores", "fused_attn_pv") and small_attn))
+        if attn_o:
+            used = name not in ("fused_attn_small", "fused_attn_scores", "fused_attn_pv", "fused_o_resid")
+        else:
+            used = name != "fused_attn_o" and not ((name == "fused_attn_small" and not small_attn) or
+                                                   (name in ("fused_attn_scores", "fused_attn_pv") and small_attn))
         if used:
             step_kernel_ns += avg_ns * (L if per_layer else 1)
         row = {"avg_us": round(avg_ns / 1e3, 3)}

@@ -174,10 +174,45 @@ def test_7b_widths_two_layers(ctx, vk, oracle):
     assert ids.tolist() == want_ids.tolist()
 
 
-def test_long_context_decode(ctx, vk, oracle):
-    """Decode attention split over many cache chunks: head_dim 128, a 1000-token prompt, then 8 steps at kv 1001+
-    (63 chunks of 16 positions per head, merged by the last chunk's block)."""
+@pytest.mark.parametrize("small_max", ["1536", "512"])
+def test_long_context_decode(ctx, vk, oracle, monkeypatch, small_max):
+    """Decode at kv 1001..1008 (head_dim 128, a 1000-token prompt, 8 steps). With the one-kernel attention admitted
+    up to 1536 positions the blocks hold 4 passes of V rows; capped at 512 the step takes the two-kernel path:
+    8 chunks of 256 positions per head, merged by the last chunk's block."""
+    monkeypatch.setenv("VKLLM_ATTN_SMALL_MAX", small_max)
     shape = dict(n_layer=2, dim=256, n_head=2, ffn=512, vocab=1000, ctx=2048)
     ids, want_ids, err = _gpu_vs_oracle(ctx, vk, oracle, shape, seed=5, prompt_len=1000, n_steps=8, prompt_seed=6)
+    assert err.max() <= LOGIT_TOL
+    assert ids.tolist() == want_ids.tolist()
+
+
+def _device_loop(ctx, vk, shape, seed, prompt, n_steps):
+    vcfg = vk.llama_config(shape["n_layer"], shape["dim"], shape["n_head"], shape["ffn"], shape["vocab"],
+                           shape["ctx"])
+    model = vk.Model(ctx, config=vcfg, seed=seed)
+    try:
+        return model.token_loop(prompt, n_steps, want_logits=True)
+    finally:
+        model.close()
+
+
+def test_attention_and_projection_in_one_launch(ctx, vk, monkeypatch):
+    """The one-kernel attention followed by Wo + residual inside the same launch (projection workgroups wait for
+    the attention workgroups) against the two separate launches, at the 7B widths: identical ids and logits."""
+    shape = dict(n_layer=2, dim=4096, n_head=32, ffn=11008, vocab=32000, ctx=160)
+    prompt = vk.prompt_tokens(8, 20, shape["vocab"])
+    monkeypatch.setenv("VKLLM_ATTN_O", "1")
+    ids_a, logits_a = _device_loop(ctx, vk, shape, 7, prompt, 24)
+    monkeypatch.setenv("VKLLM_ATTN_O", "0")
+    ids_b, logits_b = _device_loop(ctx, vk, shape, 7, prompt, 24)
+    assert ids_a.tolist() == ids_b.tolist()
+    assert np.array_equal(logits_a.view(np.uint16), logits_b.view(np.uint16))
+
+
+def test_13b_widths_one_layer(ctx, vk, oracle):
+    """The LLaMA-2-13B widths (dim 5120, 40 heads of 128, FFN 13824, vocab 32000) on one layer: 6-token prefill,
+    then 5 greedy steps."""
+    shape = dict(n_layer=1, dim=5120, n_head=40, ffn=13824, vocab=32000, ctx=32)
+    ids, want_ids, err = _gpu_vs_oracle(ctx, vk, oracle, shape, seed=9, prompt_len=6, n_steps=5, prompt_seed=10)
     assert err.max() <= LOGIT_TOL
     assert ids.tolist() == want_ids.tolist()

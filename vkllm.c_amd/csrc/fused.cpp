@@ -40,10 +40,14 @@ struct FusedState
     // decode attention scratch: scores [H, ctx], chunk statistics [H, cmax, 2], chunk partial sums [H, cmax, hd]
     float *att_scores = nullptr, *att_stats = nullptr, *att_part = nullptr;
     uint32_t *att_count = nullptr; // per-head chunk arrivals of the merge, zero between launches
+    uint32_t *attn_sync = nullptr; // counters and flags of the attention + projection launch, zero between launches
     float *gemm_work = nullptr;    // split-K partial tiles of short-prompt prefill GEMMs
     uint32_t att_cmax = 0, att_chunk = 0;
     // decode attention in one kernel up to this many positions, in two kernels beyond (VKLLM_ATTN_SMALL_MAX)
     uint32_t attn_small_max = 0;
+    // one-kernel attention and the output projection in one launch (VKLLM_ATTN_O=1; the default is two launches,
+    // which measure faster at the 7B widths); cleared when the device cannot hold both parts' workgroups at once
+    bool attn_o = false;
     // captured single-token steps: [0] with the one-kernel attention, [1] with the two-kernel attention
     hipGraph_t graph[2] = {nullptr, nullptr};
     hipGraphExec_t exec[2] = {nullptr, nullptr};
@@ -120,7 +124,7 @@ void fused_model_release(vkllm_context *ctx, vkllm_models_llama2 *model)
         (void)hipFree(fs->step);
     if (fs->freqs)
         (void)hipFree(fs->freqs);
-    void *att[] = {fs->att_scores, fs->att_stats, fs->att_part, fs->att_count, fs->gemm_work};
+    void *att[] = {fs->att_scores, fs->att_stats, fs->att_part, fs->att_count, fs->attn_sync, fs->gemm_work};
     for (void *b : att)
         if (b)
             (void)hipFree(b);
@@ -157,13 +161,24 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         fs->att_cmax = (mp->ctx + fs->att_chunk - 1) / fs->att_chunk;
         const size_t H = mp->H, C = fs->att_cmax;
         const char *sm = getenv("VKLLM_ATTN_SMALL_MAX");
-        const uint32_t small = sm && *sm ? (uint32_t)strtoul(sm, nullptr, 10) : 1536u;
+        uint32_t small = sm && *sm ? (uint32_t)strtoul(sm, nullptr, 10) : 1536u;
+        vk::AttnDecodeArgs shape{};
+        shape.H = mp->H;
+        shape.hd = mp->hd;
+        shape.ctx = mp->ctx;
+        shape.groups = vk::attn_groups(mp->H, mp->hd, 8);
+        const uint32_t limit = vk::attn_small_limit(shape);
+        small = small < limit ? small : limit;
         fs->attn_small_max = small < mp->ctx ? small : mp->ctx;
+        const char *ao = getenv("VKLLM_ATTN_O");
+        fs->attn_o = ao && *ao == '1';
         HIP_TRY(hipMalloc(&fs->att_scores, H * mp->ctx * sizeof(float)));
         HIP_TRY(hipMalloc(&fs->att_stats, H * C * 2 * sizeof(float)));
         HIP_TRY(hipMalloc(&fs->att_part, H * C * mp->hd * sizeof(float)));
         HIP_TRY(hipMalloc(&fs->att_count, H * sizeof(uint32_t)));
         HIP_TRY(hipMemset(fs->att_count, 0, H * sizeof(uint32_t)));
+        HIP_TRY(hipMalloc(&fs->attn_sync, vk::kAttnSyncWords * sizeof(uint32_t)));
+        HIP_TRY(hipMemset(fs->attn_sync, 0, vk::kAttnSyncWords * sizeof(uint32_t)));
         HIP_TRY(hipMalloc(&fs->gemm_work, kGemmWorkElems * sizeof(float)));
     }
     FusedState *fs = mp->fs;
@@ -239,6 +254,7 @@ static hipError_t launch_decode_kernel(vkllm_context *ctx, ModelPriv *mp, Kernel
     case KID_F_ATTN_SCORES:
     case KID_F_ATTN_PV:
     case KID_F_ATTN_SMALL:
+    case KID_F_ATTN_O:
     {
         vk::AttnDecodeArgs at{};
         at.q = fs->q;
@@ -259,6 +275,18 @@ static hipError_t launch_decode_kernel(vkllm_context *ctx, ModelPriv *mp, Kernel
         at.scale = 1.0f / sqrtf((float)hd);
         if (kid == KID_F_ATTN_SMALL)
             return vk::launch_attn_small(st, at, fs->attn_small_max);
+        if (kid == KID_F_ATTN_O)
+        {
+            // attention, then h + Wo attn in the same launch
+            vk::AttnOArgs ao{};
+            ao.at = at;
+            ao.wo = ly.wo;
+            ao.resid = fs->h;
+            ao.out = resid_out ? resid_out : fs->h;
+            ao.sync = fs->attn_sync;
+            ao.err = &fs->dio->err;
+            return vk::launch_attn_o(st, ao, fs->attn_small_max, cu);
+        }
         return kid == KID_F_ATTN_SCORES ? vk::launch_attn_scores(st, at) : vk::launch_attn_pv(st, at);
     }
     case KID_F_O_RESID:
@@ -305,14 +333,29 @@ static vkllm_err_t enqueue_decode(vkllm_context *ctx, ModelPriv *mp, bool small_
     for (uint32_t l = 0; l < mp->L; ++l)
     {
         DTRY(ctx, mp, KID_F_QKV, l);
-        if (small_attn)
-            DTRY(ctx, mp, KID_F_ATTN_SMALL, l);
-        else
+        bool fused_o = false;
+        if (small_attn && mp->fs->attn_o)
         {
-            DTRY(ctx, mp, KID_F_ATTN_SCORES, l);
-            DTRY(ctx, mp, KID_F_ATTN_PV, l);
+            const hipError_t e = timed(ctx, pipeline_of(ctx, KID_F_ATTN_O),
+                                       [&]() { return launch_decode_kernel(ctx, mp, KID_F_ATTN_O, l); });
+            if (e == hipSuccess)
+                fused_o = true;
+            else if (e == hipErrorInvalidConfiguration) // not enough room for both parts: two launches from now on
+                mp->fs->attn_o = false;
+            else
+                return hip_fail(e, "launch_attn_o", __FILE__, __LINE__);
         }
-        DTRY(ctx, mp, KID_F_O_RESID, l);
+        if (!fused_o)
+        {
+            if (small_attn)
+                DTRY(ctx, mp, KID_F_ATTN_SMALL, l);
+            else
+            {
+                DTRY(ctx, mp, KID_F_ATTN_SCORES, l);
+                DTRY(ctx, mp, KID_F_ATTN_PV, l);
+            }
+            DTRY(ctx, mp, KID_F_O_RESID, l);
+        }
         DTRY(ctx, mp, KID_F_GATEUP, l);
         DTRY(ctx, mp, KID_F_DOWN_RESID, l);
     }
@@ -384,6 +427,7 @@ vkllm_err_t fused_plan_run(vkllm_context *ctx, vkllm_graph *graph)
         // the chosen id back into it
         fs->dio->offset = p->offset;
         fs->dio->token = toks[0];
+        fs->dio->err = 0;
         const uint64_t t0 = fs->trace ? host_ns() : 0;
         const bool small = p->offset + 1 <= fs->attn_small_max;
         if (ctx->device->graph_replay && !ctx->device->timing)
@@ -413,6 +457,11 @@ vkllm_err_t fused_plan_run(vkllm_context *ctx, vkllm_graph *graph)
         const uint64_t t1 = fs->trace ? host_ns() : 0;
         HIP_TRY(hipStreamSynchronize(st));
         fs->io_h[0] = ((volatile vk::DecodeIo *)fs->dio)->id;
+        if (((volatile vk::DecodeIo *)fs->dio)->err)
+        {
+            log_error("decode step at position %u: a kernel's wait for other workgroups gave up", p->offset);
+            return VKLLM_ERR_VULKAN;
+        }
         if (fs->trace)
         {
             fs->trace_steps += 1;
@@ -476,7 +525,7 @@ extern "C" vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *ctx, st
         KernelId kid;
     } families[] = {{"fused_embed", KID_F_EMBED},         {"fused_qkv_rope", KID_F_QKV},
                     {"fused_attn_scores", KID_F_ATTN_SCORES}, {"fused_attn_pv", KID_F_ATTN_PV},
-                    {"fused_attn_small", KID_F_ATTN_SMALL},
+                    {"fused_attn_small", KID_F_ATTN_SMALL}, {"fused_attn_o", KID_F_ATTN_O},
                     {"fused_o_resid", KID_F_O_RESID},     {"fused_gateup", KID_F_GATEUP},
                     {"fused_down_resid", KID_F_DOWN_RESID}, {"fused_logits", KID_F_LOGITS},
                     {"fused_argmax", KID_F_ARGMAX}};
@@ -489,6 +538,12 @@ extern "C" vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *ctx, st
     if (whole && fs->last_exec < 0)
     {
         log_error("decode_step timing needs a captured decode step (graph replay on, one single-token step run)");
+        return VKLLM_ERR_ARGS;
+    }
+    if ((kid == KID_F_ATTN_SMALL || kid == KID_F_ATTN_O) && fs->dio->offset + 1 > fs->attn_small_max)
+    {
+        log_error("%s takes at most %u positions; the last step had %u", family, fs->attn_small_max,
+                  fs->dio->offset + 1);
         return VKLLM_ERR_ARGS;
     }
     hipStream_t st = ctx->device->stream;

@@ -6,6 +6,7 @@
 // rounded with the GLOBAL max and sum of its row. Both paths keep those rounding points:
 //   short caches (one kernel, attn_decode_small_kernel): block (h, g) scores all kv keys of head h itself, reduces
 //     the softmax statistics in the block and forms the probability-weighted sum for its slice of the head's dims.
+//     attn_o_kernel runs the same blocks and the output projection in one launch.
 //   long caches (two kernels over fixed chunks of `chunk` positions): attn_scores_kernel writes fp16-rounded
 //     scores and each chunk's max and sum of exp; attn_pvc_kernel reduces those statistics (identically in every
 //     block of the head), rounds the chunk's probabilities, forms its partial sums, and the last chunk block of a
@@ -13,6 +14,8 @@
 // No kernel uses a device-wide fence (on this GPU one writes back a whole L2); kv == hd takes the reference's
 // transposed product p . V^T.
 #include <float.h>
+
+#include <algorithm>
 
 #include "device_common.h"
 #include "kernels.h"
@@ -108,29 +111,6 @@ __device__ __forceinline__ void pv_transposed(const float *pl, const uint16_t *V
         for (uint32_t k = 0; k < kv; ++k)
             acc = fmaf(pl[k], h2f(row[k]), acc);
         out[r] = f2h(acc);
-    }
-}
-
-// out[d] = fp16(sum over row groups of part[group][d]) for d < dg; `part` holds rpp rows of dg partial sums and is
-// reused as scratch. Two stages keep every thread's chain short.
-template <int NT> __device__ __forceinline__ void pv_reduce_out(float *part, uint32_t rpp, uint32_t dg, uint16_t *out)
-{
-    const uint32_t tid = threadIdx.x;
-    const uint32_t ngrp = NT / dg, d = tid % dg, grp = tid / dg;
-    float s = 0.f;
-    if (grp < ngrp)
-        for (uint32_t r = grp; r < rpp; r += ngrp)
-            s += part[r * dg + d];
-    __syncthreads();
-    if (grp < ngrp)
-        part[grp * dg + d] = s;
-    __syncthreads();
-    if (tid < dg)
-    {
-        float o = 0.f;
-        for (uint32_t k = 0; k < ngrp && k < rpp; ++k)
-            o += part[k * dg + tid];
-        out[tid] = f2h(o);
     }
 }
 
@@ -317,112 +297,309 @@ __global__ __launch_bounds__(256) void attn_pvc_kernel(AttnDecodeArgs a)
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// short caches: one kernel of 1024 threads per block (16 waves: the work is latency-bound, so each thread's share is
-// short and four waves per SIMD interleave); LDS holds kv floats of scores, then probabilities
-constexpr int kSmallThreads = 1024;
+// short caches: one block of 512 threads per (head, dim slice). The work is latency-bound: the block has its first
+// keys and V rows in flight before it knows the position, each wave reduces the softmax statistics on its own, and
+// the P.V partials are reduced inside each wave before one exchange through LDS. LDS holds kv floats of scores.
+constexpr int kSmallThreads = 512;
+constexpr int kSmallMaxPasses = 6; // V rows per thread; kv <= kSmallMaxPasses * (rows per pass)
+constexpr int kSmallRed = (kSmallThreads / 64) * 32;
 
-__device__ __forceinline__ float block16_max(float v, float *red)
+// sum over aligned segments of `seg` lanes (16, 32 or 64); the last lane of each segment holds its sum
+__device__ __forceinline__ float seg_sum(float v, uint32_t seg)
 {
-    v = wave_max_dpp(v);
-    if ((threadIdx.x & 63) == 0)
-        red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float r = red[0];
-#pragma unroll
-    for (int i = 1; i < 16; ++i)
-        r = fmaxf(r, red[i]);
-    return r;
+    v = group_sum(v, 16);
+    if (seg >= 32)
+        v = dpp_add<0x142, 0xA>(v);
+    if (seg >= 64)
+        v = dpp_add<0x143, 0xC>(v);
+    return v;
 }
-__device__ __forceinline__ float block16_sum(float v, float *red)
+
+// two fp16 outputs as one 32-bit word; agent-scope (written through to the level all XCDs share) when another
+// workgroup of the same launch reads them
+template <bool AGENT> __device__ __forceinline__ void store_pair(uint16_t *p, float a, float b)
 {
-    v = wave_sum_dpp(v);
-    if ((threadIdx.x & 63) == 0)
-        red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float r = 0.f;
+    const uint32_t v = pack2(f2h(a), f2h(b));
+    if (AGENT)
+        __hip_atomic_store((uint32_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        *(uint32_t *)p = v;
+}
+
+// the reference's transposed product (kv == hd): out[r] = fp16(sum_k p_k V[r][k]) for this block's rows, two per
+// thread
+template <bool AGENT>
+__device__ __forceinline__ void pv_transposed_pairs(const float *pl, const uint16_t *Vh, uint16_t *out, uint32_t kv,
+                                                    uint32_t hd, uint32_t d0, uint32_t dg)
+{
+    for (uint32_t r = 2 * threadIdx.x; r < dg; r += 2 * blockDim.x)
+    {
+        const uint16_t *row0 = Vh + (size_t)(d0 + r) * hd, *row1 = row0 + hd;
+        float a0 = 0.f, a1 = 0.f;
+        for (uint32_t k = 0; k < kv; ++k)
+        {
+            a0 = fmaf(pl[k], h2f(row0[k]), a0);
+            a1 = fmaf(pl[k], h2f(row1[k]), a1);
+        }
+        store_pair<AGENT>(out + r, a0, a1);
+    }
+}
+
+// Block (h, g) of the short-cache attention: all kv keys of head h scored, the softmax statistics, then the
+// probability-weighted sum of dims [g dg, (g + 1) dg) of V.
+// The first two batches of keys and two passes of V rows (512 positions at head_dim 128) are requested before the
+// position is known, at rows clamped to the cache (further V passes follow the keys); rows at or past kv never reach a score or a sum (their scores are
+// not stored and their V values are replaced by zeros, whatever the cache holds there). After the scores are in
+// LDS every wave reduces the statistics itself, so no further exchange is needed until the P.V partials.
+template <int NT, bool AGENT>
+__device__ __forceinline__ void small_block(const AttnDecodeArgs &a, uint32_t h, uint32_t g, float *sm, float *red)
+{
+    constexpr uint32_t NW = NT / 64;
+    constexpr int U = 4, UV = kSmallMaxPasses;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t dg = a.hd / a.groups, d0 = g * dg, vpr = a.hd / 8, last = a.ctx - 1;
+    // V layout: lane = (vector vl of the slice, row slot); a wave covers seg rows, the block rpp rows per pass
+    const uint32_t lpr = dg / 8, seg = 64 / lpr;
+    const uint32_t vl = lane / seg, vs = wave * seg + lane % seg, rpp = NW * seg;
+    const uint16_t *Vh = a.vc + (size_t)h * a.ctx * a.hd;
+    const u32x4 *Vv = (const u32x4 *)Vh + d0 / 8 + vl;
+    u32x4 vv[UV];
+    vv[0] = Vv[(size_t)min(vs, last) * vpr];
+    vv[1] = Vv[(size_t)min(vs + rpp, last) * vpr];
+    const KeyLayout k = key_layout<NT>(a.q + (size_t)h * a.hd, a.hd);
+    const u32x4 *Kv = (const u32x4 *)(a.kc + (size_t)h * a.ctx * a.hd);
+    const uint32_t step = k.kpp * U;
+    u32x4 ka[U], kb[U], na[U], nb[U];
+    load_keys<U>(k, Kv, k.ks, last, ka, kb);
+    load_keys<U>(k, Kv, k.ks + step, last, na, nb);
+    const uint32_t kv = a.step->offset + 1;
+    const uint32_t passes = (kv + rpp - 1) / rpp;
+    const uint32_t nit = (kv + step - 1) / step;
+    for (uint32_t it = 0; it < nit; ++it)
+    {
+        score_keys<U>(k, ka, kb, k.ks + it * step, kv, a.scale, sm);
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
-        r += red[i];
-    return r;
+        for (int u = 0; u < U; ++u)
+        {
+            ka[u] = na[u];
+            kb[u] = nb[u];
+        }
+        if (it + 2 < nit)
+            load_keys<U>(k, Kv, k.ks + (it + 2) * step, kv - 1, na, nb);
+    }
+    // V rows past the first two passes (kv > 2 rpp) once the key registers are free
+#pragma unroll
+    for (int t = 2; t < UV; ++t)
+        if ((uint32_t)t < passes)
+            vv[t] = Vv[(size_t)min(vs + rpp * t, kv - 1) * vpr];
+    __syncthreads();
+    // softmax statistics, reduced by every wave over all kv scores (same values, same order in each wave)
+    float M = -FLT_MAX;
+    for (uint32_t j = lane; j < kv; j += 64)
+        M = fmaxf(M, sm[j]);
+    M = wave_max_dpp(M);
+    float L = 0.f;
+    for (uint32_t j = lane; j < kv; j += 64)
+        L += expf(sm[j] - M);
+    L = wave_sum_dpp(L);
+    uint16_t *out = a.out + (size_t)h * a.hd + d0;
+    if (kv == a.hd)
+    {
+        __syncthreads(); // every wave has its statistics before the scores become probabilities
+        for (uint32_t j = tid; j < kv; j += NT)
+            sm[j] = h2f(f2h(expf(sm[j] - M) / L));
+        __syncthreads();
+        pv_transposed_pairs<AGENT>(sm, Vh, out, kv, a.hd, d0, dg);
+        return;
+    }
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < UV; ++t)
+    {
+        const uint32_t j = vs + rpp * t;
+        if ((uint32_t)t < passes) // block-uniform
+        {
+            const bool live = j < kv;
+            const float pj = live ? h2f(f2h(expf(sm[min(j, kv - 1)] - M) / L)) : 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+            {
+                const uint32_t v = live ? vv[t][e] : 0u;
+                acc[2 * e] = fmaf(pj, half_lo(v), acc[2 * e]);
+                acc[2 * e + 1] = fmaf(pj, half_hi(v), acc[2 * e + 1]);
+            }
+        }
+    }
+    float *part = red; // NW rows of dg partial sums
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        acc[e] = seg_sum(acc[e], seg);
+    if (lane % seg == seg - 1)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            part[wave * dg + vl * 8 + e] = acc[e];
+    __syncthreads();
+    if (2 * tid < dg)
+    {
+        float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+        for (uint32_t w = 0; w < NW; ++w)
+        {
+            o0 += part[w * dg + 2 * tid];
+            o1 += part[w * dg + 2 * tid + 1];
+        }
+        store_pair<AGENT>(out + 2 * tid, o0, o1);
+    }
+}
+
+// block b of the short-cache attention (blocks of heads >= H, and launches past the LDS's positions, do nothing)
+template <bool AGENT> __device__ __forceinline__ void small_attention(const AttnDecodeArgs &a, uint32_t b, float *sm,
+                                                                     float *red)
+{
+    uint32_t h, g;
+    block_head(b, a.groups, h, g);
+    if (h >= a.H || a.step->offset + 1 > a.small_max)
+        return;
+    small_block<kSmallThreads, AGENT>(a, h, g, sm, red);
 }
 
 __global__ __launch_bounds__(kSmallThreads) void attn_decode_small_kernel(AttnDecodeArgs a)
 {
-    constexpr int NT = kSmallThreads;
     extern __shared__ float sm[];
-    __shared__ float rmax[16], rsum[16];
-    __shared__ float part[NT * 8];
-    uint32_t h, g;
-    block_head(blockIdx.x, a.groups, h, g);
-    if (h >= a.H)
-        return;
-    const uint32_t tid = threadIdx.x;
-    const uint32_t kv = a.step->offset + 1;
-    const uint16_t *Vh = a.vc + (size_t)h * a.ctx * a.hd;
-    const uint32_t dg = a.hd / a.groups, d0 = g * dg;
-    const uint32_t lpr = dg / 8, vpr = a.hd / 8, rpp = NT / lpr;
-    const uint32_t vl = tid % lpr, vs = tid / lpr;
-    const u32x4 *Vv = (const u32x4 *)Vh + d0 / 8 + vl;
-    // the block's first V rows are in flight while the keys are scored
-    constexpr int UV = 1, U = 4;
-    u32x4 vv[UV];
-#pragma unroll
-    for (int t = 0; t < UV; ++t)
-        vv[t] = Vv[(size_t)min(vs + rpp * t, kv - 1) * vpr];
-    const KeyLayout k = key_layout<NT>(a.q + (size_t)h * a.hd, a.hd);
-    const u32x4 *Kv = (const u32x4 *)(a.kc + (size_t)h * a.ctx * a.hd);
-    for (uint32_t jb = k.ks; jb < kv; jb += k.kpp * U)
+    __shared__ float red[kSmallRed];
+    small_attention<false>(a, blockIdx.x, sm, red);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Short-cache attention and the output projection with its residual add (src/models/vkllm_llama2_layers.c:247-301)
+// in one launch. The projection's 2 D^2 bytes of weights do not depend on the attention output, so they stream
+// from HBM while the (latency-bound) attention runs:
+//   blocks [0, A): the attention blocks above. Each writes its slice of the attention output with agent-scope
+//     stores and waits for them to complete; then block b counts one arrival in counter b % 8, the last arrival of
+//     each counter counts one in `top`, and the last of those raises `ready`. (Arrivals spread over 8 counters and
+//     a flag that only the waiting side reads keep the atomics from queueing behind each other and the polls.)
+//   blocks [A, grid): Wo rows, two per wave unit. After about a microsecond (the attention's own cache reads go
+//     first) the first unit's weights are requested; thread 0 then waits (bounded) for `ready`, the block reads the
+//     attention output with agent-scope loads, and the rows are finished as the separate GEMV does:
+//     out[r] = fp16(resid[r] + fp16(Wo[r] . attn)). The last of these blocks to finish clears the counters.
+// Attention blocks never wait, and the launcher sizes the grid so that every block is resident at once. A wait that
+// gives up sets *err (the step's outputs are then not valid).
+constexpr uint32_t kSpinLimit = 1u << 18;
+// sync words: arrival counters at kSyncStride c (c < 8), then top, ready and done, each on its own 256 bytes
+constexpr uint32_t kSyncStride = 64;
+constexpr uint32_t kSyncTop = 8 * kSyncStride, kSyncReady = 9 * kSyncStride, kSyncDone = 10 * kSyncStride;
+static_assert(kSyncDone < kAttnSyncWords, "sync words");
+
+template <int NV> __global__ __launch_bounds__(kSmallThreads, 4) void attn_o_kernel(AttnOArgs a)
+{
+    extern __shared__ float sm[]; // attention: kv scores; projection: the attention output (D halves)
+    __shared__ float red[kSmallRed];
+    __shared__ uint32_t gave_up;
+    constexpr uint32_t NW = kSmallThreads / 64;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint32_t *const top = a.sync + kSyncTop, *const ready = a.sync + kSyncReady, *const done = a.sync + kSyncDone;
+    const uint32_t A = a.attn_blocks;
+    if (blockIdx.x < A)
     {
-        u32x4 ka[U], kb[U];
-        load_keys<U>(k, Kv, jb, kv - 1, ka, kb);
-        score_keys<U>(k, ka, kb, jb, kv, a.scale, sm);
-    }
-    __syncthreads();
-    float mx = -FLT_MAX;
-    for (uint32_t j = tid; j < kv; j += NT)
-        mx = fmaxf(mx, sm[j]);
-    const float M = block16_max(mx, rmax);
-    float sum = 0.f;
-    for (uint32_t j = tid; j < kv; j += NT)
-        sum += expf(sm[j] - M);
-    const float L = block16_sum(sum, rsum);
-    for (uint32_t j = tid; j < kv; j += NT)
-        sm[j] = h2f(f2h(expf(sm[j] - M) / L));
-    __syncthreads();
-    uint16_t *out = a.out + (size_t)h * a.hd + d0;
-    if (kv == a.hd)
-    {
-        pv_transposed(sm, Vh, out, kv, a.hd, d0, dg);
-        return;
-    }
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (uint32_t jb = vs; jb < kv; jb += rpp * UV)
-    {
-        if (jb != vs)
+        small_attention<true>(a.at, blockIdx.x, sm, red);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0)
         {
-#pragma unroll
-            for (int t = 0; t < UV; ++t)
-                vv[t] = Vv[(size_t)min(jb + rpp * t, kv - 1) * vpr];
+            const uint32_t c = blockIdx.x % 8, groups = A < 8 ? A : 8;
+            const uint32_t in_c = A / 8 + (c < A % 8 ? 1u : 0u); // attention blocks counted by counter c
+            if (__hip_atomic_fetch_add(a.sync + kSyncStride * c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                    in_c - 1 &&
+                __hip_atomic_fetch_add(top, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == groups - 1)
+                __hip_atomic_store(ready, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+        return;
+    }
+    const uint32_t D = a.at.H * a.at.hd, nvec = D / 8, units = D / 2;
+    const uint32_t nblk = gridDim.x - A, stride = nblk * NW;
+    uint32_t u = (blockIdx.x - A) * NW + wave;
+    u32x4 w[2][NV];
+    auto load_unit = [&](uint32_t unit) {
 #pragma unroll
-        for (int t = 0; t < UV; ++t)
+        for (int k = 0; k < 2; ++k)
         {
-            const uint32_t j = jb + rpp * t;
-            const float pj = j < kv ? sm[min(j, kv - 1)] : 0.f;
+            // rows of units past the end read row 0; their sums are never stored
+            const uint32_t row = unit < units ? 2 * unit + k : 0;
+            const u32x4 *wr = (const u32x4 *)(a.wo + (size_t)row * D);
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
+            for (int i = 0; i < NV; ++i)
+                w[k][i] = __builtin_nontemporal_load(wr + min(lane + 64 * i, nvec - 1));
+        }
+    };
+    {
+        // about 1 us of the 100 MHz wall clock (bounded), so that the attention's reads are queued first
+        const uint64_t t0 = wall_clock64();
+        for (int i = 0; i < 64 && wall_clock64() - t0 < 100; ++i)
+            __builtin_amdgcn_s_sleep(2);
+    }
+    load_unit(u);
+    if (tid == 0)
+    {
+        uint32_t spins = 0, failed = 0;
+        while (__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u)
+        {
+            if (++spins >= kSpinLimit)
             {
-                acc[2 * e] = fmaf(pj, half_lo(vv[t][e]), acc[2 * e]);
-                acc[2 * e + 1] = fmaf(pj, half_hi(vv[t][e]), acc[2 * e + 1]);
+                failed = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        gave_up = failed;
+    }
+    __syncthreads();
+    uint32_t *xs = (uint32_t *)sm;
+    const uint32_t *src = (const uint32_t *)a.at.out;
+    for (uint32_t j = tid; j < D / 2; j += kSmallThreads)
+        xs[j] = __hip_atomic_load(src + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const u32x4 *xv = (const u32x4 *)sm;
+    while (u < units)
+    {
+        float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+        {
+            const uint32_t vi = lane + 64 * i;
+            if (vi < nvec)
+            {
+                const u32x4 x = xv[vi];
+                acc0 = dot8(w[0][i], x, acc0);
+                acc1 = dot8(w[1][i], x, acc1);
             }
         }
+        const uint32_t r = 2 * u;
+        u += stride;
+        if (u < units)
+            load_unit(u);
+        acc0 = wave_sum_dpp(acc0);
+        acc1 = wave_sum_dpp(acc1);
+        if (lane == 0)
+        {
+            a.out[r] = f2h(h2f(a.resid[r]) + h2f(f2h(acc0)));
+            a.out[r + 1] = f2h(h2f(a.resid[r + 1]) + h2f(f2h(acc1)));
+        }
     }
-    if (vs < rpp)
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-            part[vs * dg + vl * 8 + e] = acc[e]; // rpp * dg <= NT * 8
+    // every block of the launch has passed its wait once all projection blocks are here: clear for the next launch
     __syncthreads();
-    pv_reduce_out<NT>(part, rpp, dg, out);
+    if (tid == 0)
+    {
+        if (gave_up)
+            __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        if (__hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nblk - 1)
+        {
+            for (uint32_t c = 0; c < 8; ++c)
+                __hip_atomic_store(a.sync + kSyncStride * c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(top, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(ready, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -459,12 +636,89 @@ hipError_t launch_attn_pv(hipStream_t st, const AttnDecodeArgs &a)
     return hipGetLastError();
 }
 
+uint32_t attn_small_limit(const AttnDecodeArgs &a)
+{
+    if (!attn_args_ok(a))
+        return 0;
+    // the slice's 16-byte vectors per row must split a wave evenly, and the P.V exchange holds 32 dims per wave
+    const uint32_t lpr = a.hd / a.groups / 8;
+    if (lpr != 1 && lpr != 2 && lpr != 4)
+        return 0;
+    return kSmallMaxPasses * (kSmallThreads / lpr);
+}
+
+static uint32_t small_blocks(const AttnDecodeArgs &a)
+{
+    return (a.H + 7) / 8 * 8 * a.groups;
+}
+
 hipError_t launch_attn_small(hipStream_t st, const AttnDecodeArgs &a, uint32_t kv_max)
 {
-    if (!attn_args_ok(a) || kv_max == 0 || kv_max > a.ctx)
+    if (kv_max == 0 || kv_max > a.ctx || kv_max > attn_small_limit(a))
         return hipErrorInvalidValue;
-    attn_decode_small_kernel<<<(a.H + 7) / 8 * 8 * a.groups, kSmallThreads, (size_t)kv_max * sizeof(float), st>>>(a);
+    AttnDecodeArgs b = a;
+    b.small_max = kv_max;
+    attn_decode_small_kernel<<<small_blocks(a), kSmallThreads, (size_t)kv_max * sizeof(float), st>>>(b);
     return hipGetLastError();
+}
+
+// smallest compiled NV (16-byte vectors per lane and row) covering K = D
+static int attn_o_nv(uint32_t D)
+{
+    static const int nv[] = {1, 2, 4, 8, 10};
+    for (int v : nv)
+        if ((uint32_t)v * 64 * 8 >= D)
+            return v;
+    return 0;
+}
+
+template <int NV> static hipError_t launch_attn_o_nv(hipStream_t st, AttnOArgs a, uint32_t kv_max, int cu_count)
+{
+    const uint32_t D = a.at.H * a.at.hd;
+    const size_t lds = std::max((size_t)kv_max * sizeof(float), (size_t)D * 2);
+    // resident blocks per CU at this LDS size, cached for the last size seen
+    static size_t cached_lds = 0;
+    static int per_cu = 0;
+    if (lds != cached_lds)
+    {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_o_kernel<NV>, kSmallThreads, lds) != hipSuccess)
+            n = 0;
+        per_cu = n;
+        cached_lds = lds;
+    }
+    const uint32_t cap = (uint32_t)(cu_count > 0 ? cu_count : 256) * (uint32_t)per_cu;
+    const uint32_t A = small_blocks(a.at), units = D / 2, NW = kSmallThreads / 64;
+    if (cap <= A)
+        return hipErrorInvalidConfiguration;
+    const uint32_t B = std::min(cap - A, (units + NW - 1) / NW);
+    a.attn_blocks = A;
+    a.at.small_max = kv_max;
+    attn_o_kernel<NV><<<A + B, kSmallThreads, lds, st>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_o(hipStream_t st, const AttnOArgs &a, uint32_t kv_max, int cu_count)
+{
+    const uint32_t D = a.at.H * a.at.hd;
+    if (kv_max == 0 || kv_max > a.at.ctx || kv_max > attn_small_limit(a.at) || !a.wo || !a.resid || !a.out ||
+        !a.sync || !a.err)
+        return hipErrorInvalidValue;
+    switch (attn_o_nv(D))
+    {
+    case 1:
+        return launch_attn_o_nv<1>(st, a, kv_max, cu_count);
+    case 2:
+        return launch_attn_o_nv<2>(st, a, kv_max, cu_count);
+    case 4:
+        return launch_attn_o_nv<4>(st, a, kv_max, cu_count);
+    case 8:
+        return launch_attn_o_nv<8>(st, a, kv_max, cu_count);
+    case 10:
+        return launch_attn_o_nv<10>(st, a, kv_max, cu_count);
+    default:
+        return hipErrorInvalidValue;
+    }
 }
 
 } // namespace vk

@@ -4,10 +4,11 @@
 // Q/K/V, RoPE output, scores, probabilities, attention output, projection outputs, residual sums, SiLU(gate),
 // up*gate, logits), so fusing changes only fp32 summation order.
 //
-// Decode (one token) runs six kernels per layer:
+// Decode (one token) runs five kernels per layer (six beyond the one-kernel attention's cache length):
 //   gemv<QKV>      RMSNorm prologue, [Wq;Wk;Wv] rows, RoPE on q/k, k/v appended to the caches
-//   attn_scores    scores and per-chunk softmax statistics, split over the cache positions
-//   attn_pv        probabilities with the row's statistics, P.V per chunk, chunk merge by the last block
+//   attention      short caches: one kernel per step (attn_decode_small); long caches: attn_scores (scores and
+//                  per-chunk softmax statistics) then attn_pv (probabilities with the row's statistics, P.V per
+//                  chunk, chunk merge by the last block)
 //   gemv<RESID>    Wo rows, residual add in place
 //   gemv<GATEUP>   RMSNorm prologue, up and gate rows side by side, SiLU(gate)*up
 //   gemv<RESID>    Wd rows, residual add in place

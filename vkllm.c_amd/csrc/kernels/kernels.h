@@ -55,7 +55,7 @@ struct DecodeIo
     uint32_t offset;
     uint32_t token;
     uint32_t id;
-    uint32_t pad;
+    uint32_t err; // nonzero when a kernel's bounded wait gave up during the step
 };
 // single-token step: step = {io->offset, 1}, h = embd[io->token] (ids >= V read row unk)
 hipError_t launch_embed_decode(hipStream_t st, const DecodeIo *io, Step *step, const uint16_t *embd, uint16_t *h,
@@ -112,13 +112,32 @@ struct AttnDecodeArgs
     uint32_t *count;          // [H]: chunk arrivals, zero before the first launch; the kernels leave it zero
     uint32_t H, hd, ctx, cmax, chunk, groups;
     float scale;
+    uint32_t small_max; // one-kernel attention: positions its LDS holds (set by the launchers)
 };
 // dim slices per head: the largest divisor of hd / 8 up to max_groups with H * groups <= 1024
 uint32_t attn_groups(uint32_t H, uint32_t hd, uint32_t max_groups);
 hipError_t launch_attn_scores(hipStream_t st, const AttnDecodeArgs &a);
 hipError_t launch_attn_pv(hipStream_t st, const AttnDecodeArgs &a);
-// kv <= kv_max <= ctx; kv_max sizes the LDS
+// largest kv the one-kernel attention takes for this shape (0: the shape needs the two-kernel path)
+uint32_t attn_small_limit(const AttnDecodeArgs &a);
+// kv <= kv_max <= min(ctx, attn_small_limit); kv_max sizes the LDS
 hipError_t launch_attn_small(hipStream_t st, const AttnDecodeArgs &a, uint32_t kv_max);
+
+// One-kernel attention followed in the same launch by out[r] = fp16(resid[r] + fp16(Wo[r] . attn)) for r < H*hd
+// (K = H*hd); at.out receives the attention output. hipErrorInvalidConfiguration when the device cannot hold the
+// attention blocks and projection blocks at once (then launch them separately).
+constexpr uint32_t kAttnSyncWords = 1024;
+struct AttnOArgs
+{
+    AttnDecodeArgs at;
+    const uint16_t *wo;    // [H*hd, H*hd]
+    const uint16_t *resid; // residual stream in
+    uint16_t *out;         // residual stream out (may be resid)
+    uint32_t *sync;        // [kAttnSyncWords] zero before the first launch; every launch leaves them zero
+    uint32_t *err;         // set to 1 (system scope) when a wait gave up
+    uint32_t attn_blocks;  // set by the launcher
+};
+hipError_t launch_attn_o(hipStream_t st, const AttnOArgs &a, uint32_t kv_max, int cu_count);
 
 // prefill: queries s < S at positions offset+s attend to positions <= offset+s
 hipError_t launch_attn_prefill(hipStream_t st, const uint16_t *q, const uint16_t *kc, const uint16_t *vc,

@@ -53,6 +53,7 @@ enum KernelId
     KID_F_ATTN_PREFILL,
     KID_F_SWIGLU,
     KID_F_ATTN_SMALL,
+    KID_F_ATTN_O,
     KID_COUNT
 };
 
