@@ -216,3 +216,54 @@ def test_13b_widths_one_layer(ctx, vk, oracle):
     ids, want_ids, err = _gpu_vs_oracle(ctx, vk, oracle, shape, seed=9, prompt_len=6, n_steps=5, prompt_seed=10)
     assert err.max() <= LOGIT_TOL
     assert ids.tolist() == want_ids.tolist()
+
+
+def _steps_vs_oracle(ctx, vk, oracle, shape, seed, chunks, prompt_seed):
+    """Prefill chunks (token counts) back to back at growing offsets on a device-initialised model and on the
+    oracle; per chunk: ids and the logits of every row."""
+    cfg = oracle.make_cfg(**shape)
+    toks = oracle.prompt_tokens(prompt_seed, sum(chunks), cfg.vocab)
+    ref = oracle.Model(cfg=cfg, seed=seed)
+    vcfg = vk.llama_config(shape["n_layer"], shape["dim"], shape["n_head"], shape["ffn"], shape["vocab"],
+                           shape["ctx"])
+    model = vk.Model(ctx, config=vcfg, seed=seed)
+    out = []
+    try:
+        offset = 0
+        for n in chunks:
+            part = toks[offset:offset + n]
+            want_ids, want_logits, _ = ref.step(part, offset, want_logits=True)
+            ids = model.step(part, offset)
+            logits = model.last_logits(n)
+            out.append((ids, want_ids, logits, want_logits))
+            offset += n
+    finally:
+        ref.close()
+        model.close()
+    return out
+
+
+def test_prefill_transposed_rule_head_dim_128(ctx, vk, oracle):
+    """A 128-token prompt at head_dim 128 makes kv == hd (the reference's attn . V^T), on the MFMA prefill path;
+    then two single-token steps."""
+    shape = dict(n_layer=2, dim=256, n_head=2, ffn=512, vocab=1000, ctx=256)
+    for ids, want_ids, logits, want_logits in _steps_vs_oracle(ctx, vk, oracle, shape, 11, [128], 12):
+        err = np.max(np.abs(logits.astype(np.float32) - want_logits.astype(np.float32)))
+        print(f"max|dlogit| {err:.3g}")
+        assert err <= LOGIT_TOL
+        assert ids.tolist() == want_ids.tolist()
+    ids, want_ids, err = _gpu_vs_oracle(ctx, vk, oracle, shape, seed=11, prompt_len=128, n_steps=3, prompt_seed=12)
+    assert err.max() <= LOGIT_TOL
+    assert ids.tolist() == want_ids.tolist()
+
+
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_chunked_prefill(ctx, vk, oracle, head_dim):
+    """Prompt chunks at offsets 0, 40 and 130 (rows of a chunk attend to all earlier positions, the row max taken
+    over the whole chunk's kv), partial 64-row blocks and key blocks, on the MFMA prefill path."""
+    shape = dict(n_layer=2, dim=4 * head_dim, n_head=4, ffn=640, vocab=1000, ctx=512)
+    for ids, want_ids, logits, want_logits in _steps_vs_oracle(ctx, vk, oracle, shape, 13, [40, 90, 77], 14):
+        err = np.max(np.abs(logits.astype(np.float32) - want_logits.astype(np.float32)))
+        print(f"max|dlogit| {err:.3g}")
+        assert err <= LOGIT_TOL
+        assert ids.tolist() == want_ids.tolist()

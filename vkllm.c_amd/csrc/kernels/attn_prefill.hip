@@ -1,0 +1,279 @@
+// Prefill attention on CDNA4 matrix cores: the S query rows of a step against the kv = offset + S cached positions
+// of each head (src/models/vkllm_llama2_layers.c:223-257 with src/shaders/vkllm_softmax.comp:42-96), keeping the
+// reference's rounding points: s_j = fp16(scale * q.k_j); M = max over the WHOLE row (j < kv, later positions
+// included, as the softmax shader takes it); L = sum of exp(s_j - M) over j <= the row's position;
+// p_j = fp16(exp(s_j - M) / L) there and 0 past it; out = fp16(sum_j p_j v_j). When kv == hd the reference reads the
+// V slice as [N, K] and the product becomes out[n] = fp16(sum_k p_k V[n][k]) (src/core/vkllm_op_matmul.c:14-24).
+//
+// A workgroup of 4 waves takes 64 query rows of one head; wave w owns rows [16 w, 16 w + 16), so every row's
+// statistics stay inside one wave. Key blocks of 64 positions go through LDS (K as [key][dim], V as [dim][key]),
+// shared by the 4 waves. Products use v_mfma_f32_16x16x32_f16 in the transposed orientation:
+//   S^T = K . Q^T   (A = a 16-key slice of the K tile, B = the wave's Q rows held in registers)
+//   O^T += V^T . P^T (A = the V tile read as [dim][key], B = the probabilities straight from the S^T
+//                     accumulators: the 32 keys of a K slice are ordered so that lane l's 8 slots are the 4 keys
+//                     of each of two 16-key score blocks that it holds)
+// Pass 1 walks all kv positions for M and L (an online sum, rescaled when the row max grows); pass 2 recomputes
+// the same scores (same instructions, same order, so the same fp16 values) for the blocks at or before the last
+// row's position and accumulates P.V.
+#include <float.h>
+
+#include "device_common.h"
+#include "kernels.h"
+
+namespace vk
+{
+
+typedef _Float16 f16x8a __attribute__((ext_vector_type(8)));
+typedef float f32x4a __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kPfRows = 64; // query rows per workgroup
+constexpr uint32_t kPfKeys = 64; // positions per key block
+
+// max / sum over the 4 lanes that hold one row (lanes l, l ^ 16, l ^ 32, l ^ 48)
+__device__ __forceinline__ float row4_max(float v)
+{
+    v = fmaxf(v, __shfl_xor(v, 16));
+    return fmaxf(v, __shfl_xor(v, 32));
+}
+__device__ __forceinline__ float row4_sum(float v)
+{
+    v += __shfl_xor(v, 16);
+    return v + __shfl_xor(v, 32);
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *q, const uint16_t *kc,
+                                                                const uint16_t *vc, uint16_t *out, uint32_t offset,
+                                                                uint32_t S, uint32_t H, uint32_t ctx, float scale)
+{
+    constexpr int KS = HD / 32;           // 32-wide slices of the head dims (K of S^T = K . Q^T)
+    constexpr int DB = HD / 16;           // 16-wide blocks of output dims
+    constexpr int KROW = HD + 8;          // K tile row, halves (padded: the operand reads fall on distinct banks)
+    constexpr int VROW = kPfKeys + 8;     // V tile row ([dim][key]), halves
+    constexpr int KV = kPfKeys * HD / 8 / 256; // 16-byte K vectors per thread per block
+    constexpr int VP = 32 * (HD / 8) / 256;    // (key pair, dim chunk) items per thread per block
+    constexpr int VT = HD * (kPfKeys / 8) / 256; // transposed rule: (row, key chunk) vectors per thread
+    __shared__ __attribute__((aligned(16))) uint16_t Kt[kPfKeys * KROW];
+    __shared__ __attribute__((aligned(16))) uint16_t Vt[HD * VROW];
+
+    const uint32_t D = H * HD, h = blockIdx.y;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q4 = lane >> 4, c16 = lane & 15;
+    const uint32_t row0 = blockIdx.x * kPfRows;
+    const uint32_t rowc = min(row0 + wave * 16 + c16, S - 1); // this lane's query row (rows past S: not stored)
+    const uint32_t pos = offset + rowc;
+    const uint32_t kv = offset + S;
+    const bool transposed = kv == HD;
+    const uint16_t *Kh = kc + (size_t)h * ctx * HD, *Vh = vc + (size_t)h * ctx * HD;
+
+    // Q^T operand: column = this lane's row, K slot 8 q4 + i = dim 32 ks + 8 q4 + i
+    f16x8a qf[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+        qf[ks] = *(const f16x8a *)(q + (size_t)rowc * D + (size_t)h * HD + ks * 32 + 8 * q4);
+
+    // register prefetch of a block's K rows (clamped to kv - 1: positions past kv are masked, whatever they hold)
+    u32x4 kr[KV];
+    auto load_k = [&](uint32_t jb) {
+#pragma unroll
+        for (int i = 0; i < KV; ++i)
+        {
+            const uint32_t v = tid + 256 * i, key = v / (HD / 8), ch = v % (HD / 8);
+            kr[i] = *(const u32x4 *)(Kh + (size_t)min(jb + key, kv - 1) * HD + ch * 8);
+        }
+    };
+    auto store_k = [&]() {
+#pragma unroll
+        for (int i = 0; i < KV; ++i)
+        {
+            const uint32_t v = tid + 256 * i, key = v / (HD / 8), ch = v % (HD / 8);
+            *(u32x4 *)(Kt + key * KROW + ch * 8) = kr[i];
+        }
+    };
+    // S^T of the wave's 16 rows against the block's 64 keys: st[b][e] = score of key 16 b + 4 q4 + e, row c16
+    auto scores = [&](f32x4a *st) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+        {
+            st[b] = (f32x4a){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+            {
+                const f16x8a a = *(const f16x8a *)(Kt + (16 * b + c16) * KROW + ks * 32 + 8 * q4);
+                st[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[ks], st[b], 0, 0, 0);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                st[b][e] = h2f(f2h(st[b][e] * scale));
+        }
+    };
+
+    // ---- pass 1: row max over all kv positions, sum of exp over the causal ones
+    float m = -FLT_MAX, l = 0.f;
+    const uint32_t nb1 = (kv + kPfKeys - 1) / kPfKeys;
+    load_k(0);
+    for (uint32_t blk = 0; blk < nb1; ++blk)
+    {
+        const uint32_t jb = blk * kPfKeys;
+        __syncthreads();
+        store_k();
+        __syncthreads();
+        if (blk + 1 < nb1)
+            load_k(jb + kPfKeys);
+        f32x4a st[4];
+        scores(st);
+        float bm = -FLT_MAX;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (jb + 16 * b + 4 * q4 + e < kv)
+                    bm = fmaxf(bm, st[b][e]);
+        const float mn = fmaxf(m, row4_max(bm));
+        float add = 0.f;
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (jb + 16 * b + 4 * q4 + e <= pos)
+                    add += expf(st[b][e] - mn);
+        l = l * expf(m - mn) + add;
+        m = mn;
+    }
+    const float M = m, L = row4_sum(l);
+
+    // ---- pass 2: probabilities and P.V over the blocks at or before the workgroup's last row
+    const uint32_t last = offset + min(row0 + kPfRows, S) - 1;
+    const uint32_t nb2 = last / kPfKeys + 1;
+    f32x4a o[DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d)
+        o[d] = (f32x4a){0.f, 0.f, 0.f, 0.f};
+    u32x4 va[VP], vb[VP], vt[VT];
+    auto load_v = [&](uint32_t jb) {
+        if (!transposed)
+        {
+            // keys 2 p and 2 p + 1 of the block, dims [8 ch, 8 ch + 8)
+#pragma unroll
+            for (int i = 0; i < VP; ++i)
+            {
+                const uint32_t v = tid + 256 * i, p = v % 32, ch = v / 32;
+                va[i] = *(const u32x4 *)(Vh + (size_t)min(jb + 2 * p, kv - 1) * HD + ch * 8);
+                vb[i] = *(const u32x4 *)(Vh + (size_t)min(jb + 2 * p + 1, kv - 1) * HD + ch * 8);
+            }
+        }
+        else
+        {
+            // V rows n < hd, dims [jb + 8 c, jb + 8 c + 8): the tile is read as [n][k]
+#pragma unroll
+            for (int i = 0; i < VT; ++i)
+            {
+                const uint32_t v = tid + 256 * i, n = v / (kPfKeys / 8), c = v % (kPfKeys / 8);
+                vt[i] = *(const u32x4 *)(Vh + (size_t)n * HD + min(jb + 8 * c, (uint32_t)HD - 8));
+            }
+        }
+    };
+    auto store_v = [&]() {
+        if (!transposed)
+        {
+#pragma unroll
+            for (int i = 0; i < VP; ++i)
+            {
+                const uint32_t v = tid + 256 * i, p = v % 32, ch = v / 32;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                {
+                    *(uint32_t *)(Vt + (8 * ch + 2 * e) * VROW + 2 * p) = (va[i][e] & 0xffffu) | (vb[i][e] << 16);
+                    *(uint32_t *)(Vt + (8 * ch + 2 * e + 1) * VROW + 2 * p) = (va[i][e] >> 16) | (vb[i][e] & 0xffff0000u);
+                }
+            }
+        }
+        else
+        {
+#pragma unroll
+            for (int i = 0; i < VT; ++i)
+            {
+                const uint32_t v = tid + 256 * i, n = v / (kPfKeys / 8), c = v % (kPfKeys / 8);
+                *(u32x4 *)(Vt + n * VROW + 8 * c) = vt[i];
+            }
+        }
+    };
+    load_k(0);
+    load_v(0);
+    for (uint32_t blk = 0; blk < nb2; ++blk)
+    {
+        const uint32_t jb = blk * kPfKeys;
+        __syncthreads();
+        store_k();
+        store_v();
+        __syncthreads();
+        if (blk + 1 < nb2)
+        {
+            load_k(jb + kPfKeys);
+            load_v(jb + kPfKeys);
+        }
+        f32x4a st[4];
+        scores(st);
+        _Float16 ph[4][4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+            {
+                const bool live = jb + 16 * b + 4 * q4 + e <= pos;
+                const uint16_t p = f2h(expf(st[b][e] - M) / L);
+                _Float16 f;
+                __builtin_memcpy(&f, &p, 2);
+                ph[b][e] = live ? f : (_Float16)0.f;
+            }
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+        {
+            // K slots 8 q4 + i: keys 32 t + 4 q4 + i (i < 4) and 32 t + 16 + 4 q4 + (i - 4)
+            const f16x8a pb = {ph[2 * t][0],     ph[2 * t][1],     ph[2 * t][2],     ph[2 * t][3],
+                               ph[2 * t + 1][0], ph[2 * t + 1][1], ph[2 * t + 1][2], ph[2 * t + 1][3]};
+#pragma unroll
+            for (int d = 0; d < DB; ++d)
+            {
+                const uint16_t *vr = Vt + (16 * d + c16) * VROW + 32 * t + 4 * q4;
+                const uint2 lo = *(const uint2 *)vr, hi = *(const uint2 *)(vr + 16);
+                f16x8a a;
+                const u32x4 w = {lo.x, lo.y, hi.x, hi.y};
+                __builtin_memcpy(&a, &w, 16);
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, o[d], 0, 0, 0);
+            }
+        }
+    }
+    // O^T accumulators: o[d][e] = out[row c16][dim 16 d + 4 q4 + e]
+    const uint32_t row = row0 + wave * 16 + c16;
+    if (row < S)
+    {
+        uint16_t *orow = out + (size_t)row * D + (size_t)h * HD;
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+        {
+            const uint2 w = {pack2(f2h(o[d][0]), f2h(o[d][1])), pack2(f2h(o[d][2]), f2h(o[d][3]))};
+            *(uint2 *)(orow + 16 * d + 4 * q4) = w;
+        }
+    }
+}
+
+bool attn_prefill_mfma_ok(uint32_t hd)
+{
+    return hd == 64 || hd == 128;
+}
+
+hipError_t launch_attn_prefill_mfma(hipStream_t st, const uint16_t *q, const uint16_t *kc, const uint16_t *vc,
+                                    uint16_t *out, uint32_t offset, uint32_t S, uint32_t H, uint32_t hd, uint32_t ctx,
+                                    float scale)
+{
+    if (S == 0 || offset + S > ctx || !attn_prefill_mfma_ok(hd))
+        return hipErrorInvalidValue;
+    const dim3 grid((S + kPfRows - 1) / kPfRows, H);
+    if (hd == 128)
+        attn_prefill_mfma_kernel<128><<<grid, 256, 0, st>>>(q, kc, vc, out, offset, S, H, ctx, scale);
+    else
+        attn_prefill_mfma_kernel<64><<<grid, 256, 0, st>>>(q, kc, vc, out, offset, S, H, ctx, scale);
+    return hipGetLastError();
+}
+
+} // namespace vk

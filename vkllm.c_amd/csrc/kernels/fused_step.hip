@@ -617,12 +617,13 @@ hipError_t launch_gemv(hipStream_t st, int epi, const GemvArgs &a, int cu_count)
 
 // ---------------------------------------------------------------------------------------------------------------
 // Attention for one query row of one head (src/models/vkllm_llama2_layers.c:223-257 with
-// src/shaders/vkllm_softmax.comp:42-96): s_j = fp16(scale * q.k_j), j < kv; p = fp16(exp(s - max) / sum);
-// out[d] = fp16(sum_j p_j V[j][d]) for d in [d0, d0 + dn); with `transposed`, out[n] = fp16(sum_k p_k V[n][k]).
-// `sm` holds kv floats. All 256 threads of the block take part.
+// src/shaders/vkllm_softmax.comp:42-96): s_j = fp16(scale * q.k_j), j < kv; max over all kv scores (the softmax
+// shader's row max includes the masked positions); sum and p = fp16(exp(s - max) / sum) over j < causal, p = 0
+// beyond; out[d] = fp16(sum_j p_j V[j][d]) for d in [d0, d0 + dn); with `transposed`, out[n] = fp16(sum_k p_k
+// V[n][k]). `sm` holds kv floats. All 256 threads of the block take part.
 __device__ void attn_row(const uint16_t *q, const uint16_t *K, const uint16_t *V, uint16_t *out, uint32_t kv,
-                         uint32_t hd, float scale, bool transposed, uint32_t d0, uint32_t dn, float *sm, float *red,
-                         float *part)
+                         uint32_t causal, uint32_t hd, float scale, bool transposed, uint32_t d0, uint32_t dn,
+                         float *sm, float *red, float *part)
 {
     const uint32_t tid = threadIdx.x;
     const uint32_t vpr = hd / 8; // 16-byte vectors per cache row
@@ -660,11 +661,11 @@ __device__ void attn_row(const uint16_t *q, const uint16_t *K, const uint16_t *V
         mx = fmaxf(mx, sm[j]);
     mx = block_max(mx, red);
     float sum = 0.f;
-    for (uint32_t j = tid; j < kv; j += 256)
+    for (uint32_t j = tid; j < causal; j += 256)
         sum += expf(sm[j] - mx);
     sum = block_sum(sum, red);
     for (uint32_t j = tid; j < kv; j += 256)
-        sm[j] = h2f(f2h(expf(sm[j] - mx) / sum));
+        sm[j] = j < causal ? h2f(f2h(expf(sm[j] - mx) / sum)) : 0.f;
     __syncthreads();
 
     if (transposed)
@@ -721,7 +722,8 @@ __device__ void attn_row(const uint16_t *q, const uint16_t *K, const uint16_t *V
     }
 }
 
-// prefill: one workgroup per (query row, head); the transposition rule applies when the step's kv == hd
+// prefill for head sizes without an MFMA kernel: one workgroup per (query row, head); the transposition rule
+// applies when the step's kv == hd
 __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t *q, const uint16_t *kc, const uint16_t *vc,
                                                            uint16_t *out, uint32_t offset, uint32_t S, uint32_t H,
                                                            uint32_t hd, uint32_t ctx, float scale)
@@ -734,7 +736,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t *q, co
     const size_t hoff = (size_t)head * ctx * hd;
     const bool transposed = offset + S == hd;
     attn_row(q + (size_t)s * D + (size_t)head * hd, kc + hoff, vc + hoff, out + (size_t)s * D + (size_t)head * hd,
-             offset + s + 1, hd, scale, transposed, 0, hd, sm, red, part);
+             offset + S, offset + s + 1, hd, scale, transposed, 0, hd, sm, red, part);
 }
 
 hipError_t launch_attn_prefill(hipStream_t st, const uint16_t *q, const uint16_t *kc, const uint16_t *vc,
@@ -743,6 +745,8 @@ hipError_t launch_attn_prefill(hipStream_t st, const uint16_t *q, const uint16_t
 {
     if (hd % 8 != 0 || hd > 256)
         return hipErrorInvalidValue;
+    if (attn_prefill_mfma_ok(hd))
+        return launch_attn_prefill_mfma(st, q, kc, vc, out, offset, S, H, hd, ctx, scale);
     const size_t lds = (size_t)(offset + S) * sizeof(float);
     attn_prefill_kernel<<<dim3(S, H), 256, lds, st>>>(q, kc, vc, out, offset, S, H, hd, ctx, scale);
     return hipGetLastError();

@@ -153,6 +153,148 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint16_t *__restrict__ 
             }
 }
 
+// The same product on v_mfma_f32_32x32x16_f16 with larger wave tiles: 4 waves as 2 x 2 of (BM/2) x (BN/2), each a
+// grid of 32x32 MFMA blocks (up to 4 x 4: 256 fp32 accumulators per lane). A wave tile of 128 x 128 reads half the
+// LDS bytes per flop of a 64 x 64 one. Operands: lane l holds row (l % 32) of a 32-row block at K offset
+// 8 (l / 32) of each 16-wide K slice; the block's accumulator element e of lane l is C[8 (e / 4) + 4 (l / 32) +
+// e % 4][l % 32]. Loads, LDS layout, tile order and split-K as in gemm_kernel.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int BM, int BN, int EPI, bool SPLIT>
+__global__ __launch_bounds__(256, 1) void gemm32_kernel(const uint16_t *__restrict__ A,
+                                                        const uint16_t *__restrict__ B, uint16_t *C, float *work,
+                                                        uint32_t M, uint32_t N, uint32_t K, uint32_t ldc,
+                                                        uint32_t split, uint32_t kchunk, uint32_t tiles_m,
+                                                        uint32_t tiles_total)
+{
+    constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
+    constexpr int AV = BM * kBK / 8 / 256, BV = BN * kBK / 8 / 256; // 16-byte vectors per thread per K step
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+    auto As = [&](int b) { return lds + b * BM * kLdsRow; };
+    auto Bs = [&](int b) { return lds + 2 * BM * kLdsRow + b * BN * kLdsRow; };
+
+    const uint32_t per_xcd = gridDim.x / 8;
+    const uint32_t t = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (t >= tiles_total)
+        return;
+    const uint32_t m0 = (t % tiles_m) * BM, n0 = (t / tiles_m) * BN;
+    const uint32_t kb = SPLIT ? blockIdx.y * kchunk : 0;
+    const uint32_t ke = SPLIT ? min(K, kb + kchunk) : K;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const uint32_t wm = wid >> 1, wn = wid & 1;
+
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                acc[i][j][e] = 0.f;
+
+    u32x4 ra[AV], rb[BV];
+    // a K step wholly inside [kb, ke) loads without masks (a select on a loaded value would be compiled into a
+    // branch around each load); only a final partial step zeroes the columns past ke
+    auto load = [&](uint32_t k0) {
+        const bool whole = k0 + kBK <= ke;
+#pragma unroll
+        for (int i = 0; i < AV; ++i)
+        {
+            const uint32_t v = tid + 256 * i, row = min(m0 + v / 8, M - 1), kk = k0 + (v % 8) * 8;
+            ra[i] = *(const u32x4 *)(A + (size_t)row * K + min(kk, K - 8));
+        }
+#pragma unroll
+        for (int i = 0; i < BV; ++i)
+        {
+            const uint32_t v = tid + 256 * i, row = min(n0 + v / 8, N - 1), kk = k0 + (v % 8) * 8;
+            rb[i] = __builtin_nontemporal_load((const u32x4 *)(B + (size_t)row * K + min(kk, K - 8)));
+        }
+        if (!whole)
+        {
+#pragma unroll
+            for (int i = 0; i < AV; ++i)
+                if (k0 + ((tid + 256 * i) % 8) * 8 >= ke)
+                    ra[i] = (u32x4){0, 0, 0, 0};
+#pragma unroll
+            for (int i = 0; i < BV; ++i)
+                if (k0 + ((tid + 256 * i) % 8) * 8 >= ke)
+                    rb[i] = (u32x4){0, 0, 0, 0};
+        }
+    };
+    auto stash = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < AV; ++i)
+        {
+            const uint32_t v = tid + 256 * i;
+            *(u32x4 *)(As(buf) + (v / 8) * kLdsRow + (v % 8) * 8) = ra[i];
+        }
+#pragma unroll
+        for (int i = 0; i < BV; ++i)
+        {
+            const uint32_t v = tid + 256 * i;
+            *(u32x4 *)(Bs(buf) + (v / 8) * kLdsRow + (v % 8) * 8) = rb[i];
+        }
+    };
+
+    load(kb);
+    stash(0);
+    __syncthreads();
+    int cur = 0;
+    for (uint32_t k0 = kb; k0 < ke; k0 += kBK)
+    {
+        const bool more = k0 + kBK < ke;
+        if (more)
+            load(k0 + kBK);
+        // the next 16-wide K slice's operands are read from LDS while this slice's MFMAs run
+        f16x8 af[2][TM], bf[2][TN];
+        auto frags = [&](int slice, int into) {
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+                af[into][i] = *(const f16x8 *)(As(cur) + (wm * WM + i * 32 + lane % 32) * kLdsRow + slice * 16 +
+                                               (lane / 32) * 8);
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                bf[into][j] = *(const f16x8 *)(Bs(cur) + (wn * WN + j * 32 + lane % 32) * kLdsRow + slice * 16 +
+                                               (lane / 32) * 8);
+        };
+        frags(0, 0);
+#pragma unroll
+        for (int sl = 0; sl < kBK / 16; ++sl)
+        {
+            if (sl + 1 < kBK / 16)
+                frags(sl + 1, (sl + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0); // keep those reads ahead of this slice's MFMAs
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[sl & 1][i], bf[sl & 1][j], acc[i][j], 0, 0,
+                                                                       0);
+        }
+        if (more)
+            stash(cur ^ 1);
+        __syncthreads();
+        cur ^= 1;
+    }
+
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+            {
+                const uint32_t m = m0 + wm * WM + i * 32 + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
+                const uint32_t n = n0 + wn * WN + j * 32 + lane % 32;
+                if (m >= M || n >= N)
+                    continue;
+                if (SPLIT)
+                    work[((size_t)blockIdx.y * M + m) * N + n] = acc[i][j][e];
+                else
+                    gemm_store(EPI, C, ldc, m, n, acc[i][j][e], split);
+            }
+}
+
 // C = epilogue(sum over z of work[z]) for split-K products, the splits added in order
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float *work, uint16_t *C, uint32_t M,
@@ -194,6 +336,52 @@ static hipError_t launch_tile(hipStream_t st, const uint16_t *A, const uint16_t 
     gemm_kernel<BM, BN, EPI, SPLIT><<<dim3(grid, SPLIT ? splits : 1), 256, lds, st>>>(A, B, C, work, M, N, K, ldc,
                                                                                      split, kchunk, tm, total);
     return hipGetLastError();
+}
+
+template <int BM, int BN, int EPI, bool SPLIT>
+static hipError_t launch_tile32(hipStream_t st, const uint16_t *A, const uint16_t *B, uint16_t *C, float *work,
+                                uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, uint32_t splits,
+                                uint32_t kchunk)
+{
+    static bool attr_set = false;
+    const size_t lds = gemm_lds<BM, BN>();
+    if (!attr_set)
+    {
+        hipError_t e = hipFuncSetAttribute((const void *)gemm32_kernel<BM, BN, EPI, SPLIT>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess)
+            return e;
+        attr_set = true;
+    }
+    const uint32_t tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN, total = tm * tn;
+    const uint32_t grid = (total + 7) / 8 * 8;
+    gemm32_kernel<BM, BN, EPI, SPLIT><<<dim3(grid, SPLIT ? splits : 1), 256, lds, st>>>(A, B, C, work, M, N, K, ldc,
+                                                                                       split, kchunk, tm, total);
+    return hipGetLastError();
+}
+
+template <int EPI>
+static hipError_t launch_reduce(hipStream_t st, const float *work, uint16_t *C, uint32_t M, uint32_t N, uint32_t ldc,
+                                uint32_t split, uint32_t splits)
+{
+    const uint64_t total = (uint64_t)M * N;
+    uint32_t grid = (uint32_t)((total + 255) / 256);
+    grid = grid > 4096 ? 4096 : grid;
+    gemm_splitk_reduce_kernel<EPI><<<grid, 256, 0, st>>>(work, C, M, N, ldc, split, splits);
+    return hipGetLastError();
+}
+
+template <int BM, int BN, int EPI>
+static hipError_t launch_shape32(hipStream_t st, const uint16_t *A, const uint16_t *B, uint16_t *C, float *work,
+                                 uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, uint32_t splits,
+                                 uint32_t kchunk)
+{
+    if (splits <= 1)
+        return launch_tile32<BM, BN, EPI, false>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
+    hipError_t e = launch_tile32<BM, BN, EPI, true>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk);
+    if (e != hipSuccess)
+        return e;
+    return launch_reduce<EPI>(st, work, C, M, N, ldc, split, splits);
 }
 
 template <int BM, int BN, int EPI>

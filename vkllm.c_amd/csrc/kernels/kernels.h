@@ -139,7 +139,12 @@ struct AttnOArgs
 };
 hipError_t launch_attn_o(hipStream_t st, const AttnOArgs &a, uint32_t kv_max, int cu_count);
 
-// prefill: queries s < S at positions offset+s attend to positions <= offset+s
+// prefill: queries s < S at positions offset+s attend to positions <= offset+s (the row max over all offset+S);
+// head sizes 64 and 128 run on the MFMA kernel, others one workgroup per (row, head)
+bool attn_prefill_mfma_ok(uint32_t hd);
+hipError_t launch_attn_prefill_mfma(hipStream_t st, const uint16_t *q, const uint16_t *kc, const uint16_t *vc,
+                                    uint16_t *out, uint32_t offset, uint32_t S, uint32_t H, uint32_t hd, uint32_t ctx,
+                                    float scale);
 hipError_t launch_attn_prefill(hipStream_t st, const uint16_t *q, const uint16_t *kc, const uint16_t *vc,
                                uint16_t *out, uint32_t offset, uint32_t S, uint32_t H, uint32_t hd, uint32_t ctx,
                                float scale);
