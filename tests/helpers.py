@@ -62,3 +62,25 @@ def argmax_tie_rule(row):
     m = row.max()
     cand = np.nonzero(row == m)[0]
     return int(min(cand, key=lambda i: (bitrev5(int(i) % 32), int(i))))
+
+
+def assert_prefill_ids(ids, want_ids, want_logits, what=""):
+    """Arg-max ids of a multi-row step against the oracle's. The last row (the token the loop feeds back) must match
+    exactly. An earlier row may differ only at a near-tie: the oracle's logit for the id picked here is within one
+    fp16 ulp of the oracle's largest logit of that row, so fp32 summation order alone decides between them.
+    Returns the number of rows that differed at such ties."""
+    ids, want_ids = list(map(int, ids)), list(map(int, want_ids))
+    assert len(ids) == len(want_ids)
+    assert ids[-1] == want_ids[-1], f"{what}: last row id {ids[-1]} != {want_ids[-1]}"
+    ties = 0
+    for r, (a, b) in enumerate(zip(ids, want_ids)):
+        if a == b:
+            continue
+        row = want_logits[r].astype(np.float32)
+        top = float(row[b])
+        assert top - float(row[a]) <= float(fp16_ulp(np.float32(top))), \
+            f"{what}: row {r} id {a} (oracle logit {row[a]}) vs {b} ({top}): not a near-tie"
+        ties += 1
+    if ties:
+        print(f"{what}: {ties} of {len(ids)} rows took the other id of a one-ulp tie")
+    return ties

@@ -57,8 +57,9 @@ struct FusedState
     uint64_t trace_steps = 0, trace_enqueue_ns = 0, trace_wait_ns = 0;
 };
 
-// split-K workspace of the prefill GEMMs: 16 MB, enough for 8 splits of a 128 x 4096 tile set
-static constexpr size_t kGemmWorkElems = (size_t)4 << 20;
+// split-K workspace of the prefill GEMMs: 64 MB of fp32 partial tiles (4 splits of a 128-row QKV product at
+// dim 5120 need 31 MB)
+static constexpr size_t kGemmWorkElems = (size_t)16 << 20;
 
 static uint64_t host_ns()
 {

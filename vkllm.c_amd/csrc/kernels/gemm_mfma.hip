@@ -1,17 +1,23 @@
-// Prefill GEMM on CDNA4 matrix cores: C[M, N] = A[M, K] . B[N, K]^T with fp16 operands and fp32 accumulation
-// (v_mfma_f32_16x16x32_f16). It replaces src/shaders/vkllm_matmul_t1.comp for the token step's weight products,
-// where A holds the step's activations (M = tokens) and B a weight matrix stored [out, in].
+// Prefill GEMM on CDNA4 matrix cores: C[M, N] = A[M, K] . B[N, K]^T with fp16 operands and fp32 accumulation.
+// It replaces src/shaders/vkllm_matmul_t1.comp for the token step's weight products, where A holds the step's
+// activations (M = tokens) and B a weight matrix stored [out, in].
 //
-// Tiling: a BM x BN output tile per 256-thread workgroup, 2 x 2 waves of (BM/2) x (BN/2) as 16x16 MFMA blocks,
-// K in steps of 64. Tiles of A and B go through two LDS buffers whose rows are padded to 144 bytes (the 16-lane
-// ds_read_b128 operand fetches then fall on distinct banks): while the MFMAs consume one buffer, the next K step's
-// global loads are in flight and land in the other, so each K step costs one barrier. Global loads are
-// unconditional at clamped addresses (a guarded load compiles to a branch and a wait per load).
+// gemm32_kernel (K a multiple of 64, every prefill product of the LLaMA-2 shapes): v_mfma_f32_32x32x16_f16 on
+// 256 x 256 or 128 x 128 tiles of 256-thread workgroups, 2 x 2 waves each owning a (BM/2) x (BN/2) grid of 32x32
+// blocks (up to 256 fp32 accumulators per lane), K in steps of 64 through two LDS buffers with rows padded to 144
+// bytes (the operand reads of 8 lanes then fall on distinct banks). A step is straight-line code whose instruction
+// stream group barriers lay out as MFMAs with, between them, the next 16-wide slice's operand reads, the next
+// step's global loads (first slice) and their stores into the other LDS buffer (last slice), so memory traffic
+// runs under the matrix pipe; one barrier per step.
+// gemm_kernel (other K): v_mfma_f32_16x16x32_f16, 128 x 128 or 128 x 64 tiles, the same double buffering, with the
+// K tail zeroed.
 //
-// Short prompts (M <= 128): one tile covers all of M so every weight is read once, and narrow products split K
-// over several workgroups so that enough of them run at once; the fp32 partial tiles are then added in split
-// order by gemm_splitk_reduce_kernel, which applies the epilogue.
-// Tiles are ordered M-fastest and dealt to XCDs in contiguous runs so a run shares its B tiles in one L2.
+// Narrow products split K over several workgroups; the fp32 partial tiles are added in split order by
+// gemm_splitk_reduce_kernel, which applies the epilogue. Tiles are ordered M-fastest and dealt to XCDs in
+// contiguous runs so a run shares its B tiles in one L2. Global loads are unconditional at clamped addresses (a
+// guarded load compiles to a branch and a wait per load).
+#include <type_traits>
+
 #include "device_common.h"
 #include "kernels.h"
 
@@ -192,33 +198,21 @@ __global__ __launch_bounds__(256, 1) void gemm32_kernel(const uint16_t *__restri
             for (int e = 0; e < 16; ++e)
                 acc[i][j][e] = 0.f;
 
+    // every K step lies wholly inside [kb, ke) (the launcher admits K ranges of whole 64-wide steps), so the
+    // loads need no masks and each step's body is straight-line code for the scheduler
     u32x4 ra[AV], rb[BV];
-    // a K step wholly inside [kb, ke) loads without masks (a select on a loaded value would be compiled into a
-    // branch around each load); only a final partial step zeroes the columns past ke
     auto load = [&](uint32_t k0) {
-        const bool whole = k0 + kBK <= ke;
 #pragma unroll
         for (int i = 0; i < AV; ++i)
         {
-            const uint32_t v = tid + 256 * i, row = min(m0 + v / 8, M - 1), kk = k0 + (v % 8) * 8;
-            ra[i] = *(const u32x4 *)(A + (size_t)row * K + min(kk, K - 8));
+            const uint32_t v = tid + 256 * i, row = min(m0 + v / 8, M - 1);
+            ra[i] = *(const u32x4 *)(A + (size_t)row * K + k0 + (v % 8) * 8);
         }
 #pragma unroll
         for (int i = 0; i < BV; ++i)
         {
-            const uint32_t v = tid + 256 * i, row = min(n0 + v / 8, N - 1), kk = k0 + (v % 8) * 8;
-            rb[i] = __builtin_nontemporal_load((const u32x4 *)(B + (size_t)row * K + min(kk, K - 8)));
-        }
-        if (!whole)
-        {
-#pragma unroll
-            for (int i = 0; i < AV; ++i)
-                if (k0 + ((tid + 256 * i) % 8) * 8 >= ke)
-                    ra[i] = (u32x4){0, 0, 0, 0};
-#pragma unroll
-            for (int i = 0; i < BV; ++i)
-                if (k0 + ((tid + 256 * i) % 8) * 8 >= ke)
-                    rb[i] = (u32x4){0, 0, 0, 0};
+            const uint32_t v = tid + 256 * i, row = min(n0 + v / 8, N - 1);
+            rb[i] = __builtin_nontemporal_load((const u32x4 *)(B + (size_t)row * K + k0 + (v % 8) * 8));
         }
     };
     auto stash = [&](int buf) {
@@ -235,47 +229,85 @@ __global__ __launch_bounds__(256, 1) void gemm32_kernel(const uint16_t *__restri
             *(u32x4 *)(Bs(buf) + (v / 8) * kLdsRow + (v % 8) * 8) = rb[i];
         }
     };
+    f16x8 af[2][TM], bf[2][TN];
+    auto frags = [&](int buf, int slice, int into) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+            af[into][i] = *(const f16x8 *)(As(buf) + (wm * WM + i * 32 + lane % 32) * kLdsRow + slice * 16 +
+                                           (lane / 32) * 8);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            bf[into][j] = *(const f16x8 *)(Bs(buf) + (wn * WN + j * 32 + lane % 32) * kLdsRow + slice * 16 +
+                                           (lane / 32) * 8);
+    };
+    auto mfmas = [&](int from) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[from][i], bf[from][j], acc[i][j], 0, 0, 0);
+    };
+    // One K step from LDS buffer `buf`. With MORE, the next step's global loads are issued during the first slice
+    // and land in the other buffer during the last one. The group barriers lay the instruction stream out as MFMAs
+    // with the operand reads of the next slice, the global loads and the LDS stores threaded between them.
+    constexpr int NMF = TM * TN, NDR = TM + TN, NLD = AV + BV;
+    constexpr int LD_PER = (NLD + NMF - 1) / NMF;
+    auto step = [&](auto more_tag, int buf, uint32_t k0) {
+        constexpr bool MORE = decltype(more_tag)::value;
+        frags(buf, 0, 0);
+        frags(buf, 1, 1);
+        if constexpr (MORE)
+            load(k0 + kBK);
+        mfmas(0);
+        frags(buf, 2, 0);
+        mfmas(1);
+        frags(buf, 3, 1);
+        mfmas(0);
+        mfmas(1);
+        if constexpr (MORE)
+            stash(buf ^ 1);
+        // slice 0 operands first, then: slice 0 MFMAs with slice 1 reads and the global loads, slices 1 and 2 with
+        // the next slice's reads, slice 3 with the LDS stores
+        __builtin_amdgcn_sched_group_barrier(0x100, NDR, 0);
+#pragma unroll
+        for (int i = 0; i < NMF; ++i)
+        {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (i < NDR)
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            if (MORE && i * LD_PER < NLD)
+                __builtin_amdgcn_sched_group_barrier(0x020, LD_PER, 0);
+        }
+#pragma unroll
+        for (int sl = 1; sl < 3; ++sl)
+#pragma unroll
+            for (int i = 0; i < NMF; ++i)
+            {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (i < NDR)
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+#pragma unroll
+        for (int i = 0; i < NMF; ++i)
+        {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (MORE && i * LD_PER < NLD)
+                __builtin_amdgcn_sched_group_barrier(0x200, LD_PER, 0);
+        }
+    };
 
     load(kb);
     stash(0);
     __syncthreads();
     int cur = 0;
-    for (uint32_t k0 = kb; k0 < ke; k0 += kBK)
+    uint32_t k0 = kb;
+    for (; k0 + kBK < ke; k0 += kBK)
     {
-        const bool more = k0 + kBK < ke;
-        if (more)
-            load(k0 + kBK);
-        // the next 16-wide K slice's operands are read from LDS while this slice's MFMAs run
-        f16x8 af[2][TM], bf[2][TN];
-        auto frags = [&](int slice, int into) {
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-                af[into][i] = *(const f16x8 *)(As(cur) + (wm * WM + i * 32 + lane % 32) * kLdsRow + slice * 16 +
-                                               (lane / 32) * 8);
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-                bf[into][j] = *(const f16x8 *)(Bs(cur) + (wn * WN + j * 32 + lane % 32) * kLdsRow + slice * 16 +
-                                               (lane / 32) * 8);
-        };
-        frags(0, 0);
-#pragma unroll
-        for (int sl = 0; sl < kBK / 16; ++sl)
-        {
-            if (sl + 1 < kBK / 16)
-                frags(sl + 1, (sl + 1) & 1);
-            __builtin_amdgcn_sched_barrier(0); // keep those reads ahead of this slice's MFMAs
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[sl & 1][i], bf[sl & 1][j], acc[i][j], 0, 0,
-                                                                       0);
-        }
-        if (more)
-            stash(cur ^ 1);
+        step(std::true_type{}, cur, k0);
         __syncthreads();
         cur ^= 1;
     }
+    step(std::false_type{}, cur, k0);
 
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -407,6 +439,22 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
                                   uint32_t split, int cu_count)
 {
     const uint32_t cus = cu_count > 0 ? (uint32_t)cu_count : 256;
+    if (K % kBK == 0)
+    {
+        // 32x32x16 kernel: 256 x 256 tiles when they alone give most CUs a tile; else 128 x 128 tiles (two fit a
+        // CU) with K split until about two workgroups per CU run, each split keeping at least 256 of K
+        const uint64_t t256 = (uint64_t)((M + 255) / 256) * ((N + 255) / 256);
+        if (t256 >= (cus * 3) / 4)
+            return launch_shape32<256, 256, EPI>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
+        const uint64_t tiles = (uint64_t)((M + 127) / 128) * ((N + 127) / 128);
+        uint32_t splits = 1;
+        while (tiles * splits * 2 <= 2 * (uint64_t)cus && K / (splits * 2) >= 256 &&
+               (size_t)splits * 2 * M * N <= work_elems)
+            splits *= 2;
+        const uint32_t kchunk = ((K + splits - 1) / splits + kBK - 1) / kBK * kBK;
+        splits = (K + kchunk - 1) / kchunk;
+        return launch_shape32<128, 128, EPI>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk);
+    }
     if (M <= 128)
     {
         // weight-streaming regime: a 128-row tile covers all of M so each weight is read once; K is split over
