@@ -400,6 +400,7 @@ extern "C" void vkllm_context_free(struct vkllm_context *ctx)
         for (hipEvent_t e : ctx->device->event_pool)
             (void)hipEventDestroy(e);
         pool_release_all(ctx->device);
+        node_pool_release(ctx->device);
         if (ctx->device->stream)
             (void)hipStreamDestroy(ctx->device->stream);
         delete ctx->device;

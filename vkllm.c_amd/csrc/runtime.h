@@ -75,6 +75,8 @@ struct vkllm_gpu_device
     // pinned host blocks (mirrors of mapped tensors), same size classes
     std::unordered_map<size_t, std::vector<void *>> pinned_free;
     std::vector<void *> pinned_all;
+    // recycled tensor structs (a token step builds and frees one per graph node)
+    std::vector<void *> node_free;
     int exec_mode = VKLLM_EXEC_FUSED;
     int graph_replay = 1;
     int timing = 0;
@@ -105,6 +107,7 @@ void pool_free(vkllm_gpu_device *dev, void *p, size_t bytes);
 void pool_release_all(vkllm_gpu_device *dev);
 void *pinned_alloc(vkllm_gpu_device *dev, size_t bytes);
 void pinned_free(vkllm_gpu_device *dev, void *p, size_t bytes);
+void node_pool_release(vkllm_gpu_device *dev);
 
 // Device address of a tensor's element [0,0,0,0]; follows views to their base and allocates the base's memory
 // on first use. nullptr on allocation failure.

@@ -26,6 +26,60 @@ static void calc_strides(const uint32_t *shapes, vkllm_dtype_t dtype, uint32_t *
     strides[0] = shapes[1] * strides[1];
 }
 
+// Tensor structs are recycled per device: a decode step builds and frees one per graph node (741 at 32 layers),
+// and a calloc/free pair per node costs more than building it. Each struct sits behind a header that records its
+// params capacity; structs of the common capacity go back to the device's free list, others to free().
+namespace
+{
+constexpr size_t kNodeParamsCap = 64;
+constexpr size_t kNodeFreeMax = 1u << 14;
+struct alignas(16) NodeHdr
+{
+    size_t params_cap;
+};
+} // namespace
+
+static vkllm_tensor *node_alloc(vkllm_gpu_device *dev, size_t params_bytes)
+{
+    const size_t cap = params_bytes <= kNodeParamsCap ? kNodeParamsCap : params_bytes;
+    const size_t total = sizeof(NodeHdr) + sizeof(vkllm_tensor) + cap;
+    NodeHdr *h = nullptr;
+    if (cap == kNodeParamsCap && dev && !dev->node_free.empty())
+    {
+        h = (NodeHdr *)dev->node_free.back();
+        dev->node_free.pop_back();
+        memset(h, 0, total);
+    }
+    else if (!(h = (NodeHdr *)calloc(1, total)))
+        return nullptr;
+    h->params_cap = cap;
+    return (vkllm_tensor *)(h + 1);
+}
+
+static void node_release(vkllm_gpu_device *dev, vkllm_tensor *t)
+{
+    NodeHdr *h = (NodeHdr *)t - 1;
+    if (h->params_cap == kNodeParamsCap && dev && dev->node_free.size() < kNodeFreeMax)
+    {
+        try
+        {
+            dev->node_free.push_back(h);
+            return;
+        }
+        catch (...)
+        {
+        }
+    }
+    free(h);
+}
+
+void node_pool_release(vkllm_gpu_device *dev)
+{
+    for (void *p : dev->node_free)
+        free(p);
+    dev->node_free.clear();
+}
+
 vkllm_tensor *tensor_base(vkllm_tensor *t)
 {
     while (t && t->data.is_ref && t->srcs[0])
@@ -88,11 +142,11 @@ extern "C" vkllm_err_t vkllm_tensor_new(struct vkllm_context *context, const cha
                   (unsigned long long)total);
         return VKLLM_ERR_ARGS;
     }
-    auto *t = (vkllm_tensor *)calloc(1, sizeof(vkllm_tensor) + params_bytes);
+    auto *t = node_alloc(context->device, params_bytes);
     if (!t)
         return VKLLM_ERR_ALLOC;
     if (name)
-        memcpy((char *)t->name, name, strnlen(name, sizeof(t->name) - 1)); // calloc left the terminator
+        memcpy((char *)t->name, name, strnlen(name, sizeof(t->name) - 1)); // the zeroed struct holds the terminator
     t->dtype = dtype;
     memcpy(t->shapes, shapes, sizeof(t->shapes));
     calc_strides(shapes, dtype, t->strides);
@@ -109,7 +163,7 @@ extern "C" vkllm_err_t vkllm_tensor_new(struct vkllm_context *context, const cha
         t->data.host = pinned_alloc(context->device, t->bytes);
         if (!t->data.host)
         {
-            free(t);
+            node_release(context->device, t);
             return VKLLM_ERR_ALLOC;
         }
         memset(t->data.host, 0, t->bytes);
@@ -120,7 +174,7 @@ extern "C" vkllm_err_t vkllm_tensor_new(struct vkllm_context *context, const cha
         if (!tensor_dev(context, t))
         {
             pinned_free(context->device, t->data.host, t->bytes);
-            free(t);
+            node_release(context->device, t);
             return VKLLM_ERR_ALLOC;
         }
     }
@@ -140,7 +194,7 @@ extern "C" void vkllm_tensor_free(struct vkllm_context *context, struct vkllm_te
         if (t->data.host)
             pinned_free(context->device, t->data.host, t->bytes);
     }
-    free(t);
+    node_release(context->device, t);
     context->stats.tensor_free_counts += 1;
 }
 
@@ -218,7 +272,7 @@ extern "C" vkllm_err_t vkllm_tensor_copy_ref(struct vkllm_context *context, stru
                                              struct vkllm_tensor **p)
 {
     _CHECK_ARGS(context && tensor && p);
-    auto *t = (vkllm_tensor *)calloc(1, sizeof(vkllm_tensor));
+    auto *t = node_alloc(context->device, 0);
     if (!t)
         return VKLLM_ERR_ALLOC;
     name_with_suffix((char *)t->name, sizeof(t->name), tensor->name, "_ref");
