@@ -243,4 +243,15 @@ __device__ __forceinline__ float block4_sum(float v, float *red)
     return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
+// RoPE rotation terms c v0 - s v1 and s v0 + c v1 (src/shaders/vkllm_rope.comp:72-75) with every product and sum
+// rounded on its own (no fused multiply-add)
+__device__ __forceinline__ float rope_mul_sub(float c, float a, float s, float b)
+{
+    return __fsub_rn(__fmul_rn(c, a), __fmul_rn(s, b));
+}
+__device__ __forceinline__ float rope_mul_add(float s, float a, float c, float b)
+{
+    return __fadd_rn(__fmul_rn(s, a), __fmul_rn(c, b));
+}
+
 } // namespace vk

@@ -145,15 +145,6 @@ hipError_t launch_rmsnorm_rows(hipStream_t st, const uint16_t *x, const float *w
 // walk the units grid-stride so the prologue (input vector, optional RMSNorm) is paid once per workgroup.
 constexpr int kGemvUnroll = 8;
 
-__device__ __forceinline__ float rope_mul_sub(float c, float a, float s, float b)
-{
-    return __fsub_rn(__fmul_rn(c, a), __fmul_rn(s, b));
-}
-__device__ __forceinline__ float rope_mul_add(float s, float a, float c, float b)
-{
-    return __fadd_rn(__fmul_rn(s, a), __fmul_rn(c, b));
-}
-
 template <int EPI> __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a)
 {
     extern __shared__ u32x4 xs[];
