@@ -300,8 +300,10 @@ template <int EPI> __device__ __forceinline__ void gemv_rows_of(const GemvArgs &
     }
 }
 
+// EPI_QKV: fq[k / 2] is the RoPE denominator of pair (rows[k], rows[k + 1]), fetched with the unit's weights
 template <int EPI, int R> __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, uint32_t u,
-                                                                        const uint32_t *rows, const float *acc)
+                                                                        const uint32_t *rows, const float *acc,
+                                                                        const float *fq)
 {
     if (EPI == EPI_PLAIN)
     {
@@ -345,7 +347,7 @@ template <int EPI, int R> __device__ __forceinline__ void gemv_epilogue(const Ge
                 a.vc[cache + 1] = f2h(v1);
                 continue;
             }
-            const float f = (float)pos / a.freqs[dim / 2];
+            const float f = (float)pos / fq[k / 2];
             const float c = cosf(f), sn = sinf(f);
             const uint16_t o0 = f2h(rope_mul_sub(c, v0, sn, v1)), o1 = f2h(rope_mul_add(sn, v0, c, v1));
             if (region == 0)
@@ -398,8 +400,19 @@ template <int EPI, int R, int NV> __global__ __launch_bounds__(256) void gemv_fa
     uint32_t u = blockIdx.x * 4 + wid;
     u32x4 w[R][NV];
     uint32_t rows[R];
+    // EPI_QKV: the unit's RoPE denominators, requested ahead of its weights (a later request would make the
+    // epilogue wait for the next unit's weights: counters retire in issue order)
+    constexpr int NF = EPI == EPI_QKV && R >= 2 ? R / 2 : 1;
+    float fq[NF];
+#pragma unroll
+    for (int k = 0; k < NF; ++k)
+        fq[k] = 1.f;
     auto load_unit = [&](uint32_t unit) {
         gemv_rows_of<EPI>(a, unit, R, rows);
+        if (EPI == EPI_QKV)
+#pragma unroll
+            for (int k = 0; k < NF; ++k)
+                fq[k] = a.freqs[((unit < units && rows[2 * k] < a.rows ? rows[2 * k] : 0) % a.D) % a.hd / 2];
 #pragma unroll
         for (int k = 0; k < R; ++k)
         {
@@ -470,9 +483,13 @@ template <int EPI, int R, int NV> __global__ __launch_bounds__(256) void gemv_fa
             }
         }
         uint32_t cur_rows[R];
+        float cur_fq[NF];
 #pragma unroll
         for (int k = 0; k < R; ++k)
             cur_rows[k] = rows[k];
+#pragma unroll
+        for (int k = 0; k < NF; ++k)
+            cur_fq[k] = fq[k];
         const uint32_t cur = u;
         u += stride;
         if (u < units)
@@ -481,7 +498,7 @@ template <int EPI, int R, int NV> __global__ __launch_bounds__(256) void gemv_fa
         for (int k = 0; k < R; ++k)
             acc[k] = wave_sum_dpp(acc[k]);
         if (lane == 0)
-            gemv_epilogue<EPI, R>(a, cur, cur_rows, acc);
+            gemv_epilogue<EPI, R>(a, cur, cur_rows, acc, cur_fq);
     }
 }
 
