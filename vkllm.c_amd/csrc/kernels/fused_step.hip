@@ -300,10 +300,11 @@ template <int EPI> __device__ __forceinline__ void gemv_rows_of(const GemvArgs &
     }
 }
 
-// EPI_QKV: fq[k / 2] is the RoPE denominator of pair (rows[k], rows[k + 1]), fetched with the unit's weights
+// Inputs of the epilogue are fetched with the unit's weights: EPI_QKV fq[k / 2], the RoPE denominator of pair
+// (rows[k], rows[k + 1]); EPI_RESID rs[k], the residual at rows[k].
 template <int EPI, int R> __device__ __forceinline__ void gemv_epilogue(const GemvArgs &a, uint32_t u,
                                                                         const uint32_t *rows, const float *acc,
-                                                                        const float *fq)
+                                                                        const float *fq, const float *rs)
 {
     if (EPI == EPI_PLAIN)
     {
@@ -317,7 +318,7 @@ template <int EPI, int R> __device__ __forceinline__ void gemv_epilogue(const Ge
 #pragma unroll
         for (int k = 0; k < R; ++k)
             if (rows[k] < a.rows)
-                a.out[rows[k]] = f2h(h2f(a.resid[rows[k]]) + h2f(f2h(acc[k])));
+                a.out[rows[k]] = f2h(rs[k] + h2f(f2h(acc[k])));
     }
     else if (EPI == EPI_GATEUP)
     {
@@ -400,19 +401,26 @@ template <int EPI, int R, int NV> __global__ __launch_bounds__(256) void gemv_fa
     uint32_t u = blockIdx.x * 4 + wid;
     u32x4 w[R][NV];
     uint32_t rows[R];
-    // EPI_QKV: the unit's RoPE denominators, requested ahead of its weights (a later request would make the
-    // epilogue wait for the next unit's weights: counters retire in issue order)
-    constexpr int NF = EPI == EPI_QKV && R >= 2 ? R / 2 : 1;
-    float fq[NF];
+    // the epilogue's inputs (RoPE denominators, residuals), requested ahead of the unit's weights: a request in the
+    // epilogue would wait for the next unit's weights, as counters retire in issue order
+    constexpr int NF = EPI == EPI_QKV && R >= 2 ? R / 2 : 1, NR = EPI == EPI_RESID ? R : 1;
+    float fq[NF], rs[NR];
 #pragma unroll
     for (int k = 0; k < NF; ++k)
         fq[k] = 1.f;
+#pragma unroll
+    for (int k = 0; k < NR; ++k)
+        rs[k] = 0.f;
     auto load_unit = [&](uint32_t unit) {
         gemv_rows_of<EPI>(a, unit, R, rows);
         if (EPI == EPI_QKV)
 #pragma unroll
             for (int k = 0; k < NF; ++k)
                 fq[k] = a.freqs[((unit < units && rows[2 * k] < a.rows ? rows[2 * k] : 0) % a.D) % a.hd / 2];
+        if (EPI == EPI_RESID)
+#pragma unroll
+            for (int k = 0; k < NR; ++k)
+                rs[k] = h2f(a.resid[unit < units && rows[k] < a.rows ? rows[k] : 0]);
 #pragma unroll
         for (int k = 0; k < R; ++k)
         {
@@ -483,13 +491,16 @@ template <int EPI, int R, int NV> __global__ __launch_bounds__(256) void gemv_fa
             }
         }
         uint32_t cur_rows[R];
-        float cur_fq[NF];
+        float cur_fq[NF], cur_rs[NR];
 #pragma unroll
         for (int k = 0; k < R; ++k)
             cur_rows[k] = rows[k];
 #pragma unroll
         for (int k = 0; k < NF; ++k)
             cur_fq[k] = fq[k];
+#pragma unroll
+        for (int k = 0; k < NR; ++k)
+            cur_rs[k] = rs[k];
         const uint32_t cur = u;
         u += stride;
         if (u < units)
@@ -498,7 +509,7 @@ template <int EPI, int R, int NV> __global__ __launch_bounds__(256) void gemv_fa
         for (int k = 0; k < R; ++k)
             acc[k] = wave_sum_dpp(acc[k]);
         if (lane == 0)
-            gemv_epilogue<EPI, R>(a, cur, cur_rows, acc, cur_fq);
+            gemv_epilogue<EPI, R>(a, cur, cur_rows, acc, cur_fq, cur_rs);
     }
 }
 
