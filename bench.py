@@ -67,6 +67,7 @@ def decode_bytes(shape, kv):
         "fused_qkv_rope": 3 * D * D * 2 + D * 2 + D * 4 + D * 2 + 2 * D * 2,
         "fused_attn_small": attn,
         "fused_attn_scores": attn,
+        "fused_attn_long": attn,
         "fused_o_resid": D * D * 2 + D * 2 + 2 * D * 2,
         "fused_attn_o": attn + D * D * 2 + 2 * D * 2,
         "fused_gateup": 2 * F * D * 2 + D * 2 + D * 4 + F * 2,
@@ -235,14 +236,29 @@ def main():
     small_attn = pos <= ATTN_SMALL_MAX  # the library's default switch-over to the two-kernel attention
     # short caches: attention and the output projection run as one launch with VKLLM_ATTN_O=1
     attn_o = small_attn and os.environ.get("VKLLM_ATTN_O", "0") == "1"
-    for name in ("fused_embed", "fused_qkv_rope", "fused_attn_o", "fused_attn_small", "fused_attn_scores",
-                 "fused_attn_pv", "fused_o_resid", "fused_gateup", "fused_down_resid", "fused_logits", "fused_argmax"):
+    # long caches: scores and P.V in one launch when the device holds every chunk block at once (the library then
+    # uses it; it refuses to time it otherwise)
+    attn_long = False
+    for name in ("fused_embed", "fused_qkv_rope", "fused_attn_o", "fused_attn_small", "fused_attn_long",
+                 "fused_attn_scores", "fused_attn_pv", "fused_o_resid", "fused_gateup", "fused_down_resid",
+                 "fused_logits", "fused_argmax"):
         per_layer = name not in ("fused_embed", "fused_logits", "fused_argmax")
         reps = 4 * L if per_layer else 32
         if name in ("fused_attn_o", "fused_attn_small") and pos > ATTN_SMALL_MAX:
             continue  # the one-kernel attention takes at most ATTN_SMALL_MAX positions
-        avg_ns = model.time_kernel(name, reps)
-        if attn_o:
+        if name == "fused_attn_long":
+            if small_attn or os.environ.get("VKLLM_ATTN_LONG", "1") == "0":
+                continue
+            try:
+                avg_ns = model.time_kernel(name, reps)
+            except vk.VkllmError:
+                continue
+            attn_long = True
+        else:
+            avg_ns = model.time_kernel(name, reps)
+        if attn_long and name in ("fused_attn_scores", "fused_attn_pv"):
+            used = False
+        elif attn_o:
             used = name not in ("fused_attn_small", "fused_attn_scores", "fused_attn_pv", "fused_o_resid")
         else:
             used = name != "fused_attn_o" and not ((name == "fused_attn_small" and not small_attn) or

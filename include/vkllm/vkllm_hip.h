@@ -38,8 +38,8 @@ extern vkllm_err_t vkllm_hip_reset_kernel_stats(struct vkllm_context *context);
 /* Launches the decode-step kernel `family` `reps` times back to back, cycling over the layers' weights, between
  * one hipEvent pair on the context's stream, and returns the elapsed nanoseconds: the kernel's duration without
  * the per-launch dispatch latency that a per-launch event pair adds. Families: "fused_embed", "fused_qkv_rope",
- * "fused_attn_scores", "fused_attn_pv", "fused_attn_small", "fused_attn_o" (one-kernel attention and Wo + residual in
- * one launch), "fused_o_resid", "fused_gateup", "fused_down_resid",
+ * "fused_attn_scores", "fused_attn_pv", "fused_attn_long" (both in one launch), "fused_attn_small", "fused_attn_o"
+ * (one-kernel attention and Wo + residual in one launch), "fused_o_resid", "fused_gateup", "fused_down_resid",
  * "fused_logits", "fused_argmax" (the embedding and residual GEMVs write into a scratch row, so repeats leave the
  * model state unchanged), and "decode_step": replays of the captured single-token graph the last step used, at
  * its position. Needs a preceding single-token step of `model`. */

@@ -176,12 +176,13 @@ def test_7b_widths_two_layers(ctx, vk, oracle):
     assert ids.tolist() == want_ids.tolist()
 
 
-@pytest.mark.parametrize("small_max", ["1536", "512"])
-def test_long_context_decode(ctx, vk, oracle, monkeypatch, small_max):
+@pytest.mark.parametrize("small_max,long_one", [("1536", "1"), ("512", "1"), ("512", "0")])
+def test_long_context_decode(ctx, vk, oracle, monkeypatch, small_max, long_one):
     """Decode at kv 1001..1008 (head_dim 128, a 1000-token prompt, 8 steps). With the one-kernel attention admitted
-    up to 1536 positions the blocks hold 4 passes of V rows; capped at 512 the step takes the two-kernel path:
-    8 chunks of 256 positions per head, merged by the last chunk's block."""
+    up to 1536 positions the blocks hold 4 passes of V rows; capped at 512 the step takes the long-cache path:
+    8 chunks of 256 positions per head, merged by the last chunk's block, in one launch or in two."""
     monkeypatch.setenv("VKLLM_ATTN_SMALL_MAX", small_max)
+    monkeypatch.setenv("VKLLM_ATTN_LONG", long_one)
     shape = dict(n_layer=2, dim=256, n_head=2, ffn=512, vocab=1000, ctx=2048)
     ids, want_ids, err = _gpu_vs_oracle(ctx, vk, oracle, shape, seed=5, prompt_len=1000, n_steps=8, prompt_seed=6)
     assert err.max() <= LOGIT_TOL
@@ -207,6 +208,21 @@ def test_attention_and_projection_in_one_launch(ctx, vk, monkeypatch):
     ids_a, logits_a = _device_loop(ctx, vk, shape, 7, prompt, 24)
     monkeypatch.setenv("VKLLM_ATTN_O", "0")
     ids_b, logits_b = _device_loop(ctx, vk, shape, 7, prompt, 24)
+    assert ids_a.tolist() == ids_b.tolist()
+    assert np.array_equal(logits_a.view(np.uint16), logits_b.view(np.uint16))
+
+
+def test_long_cache_attention_in_one_launch(ctx, vk, monkeypatch):
+    """The long-cache attention in one launch (chunk blocks wait for each other's statistics) against the scores and
+    P.V kernels, at the 7B widths with a 640-position cache (3 chunks of 224): from the first long-cache step through
+    kv == head_dim (the transposed product) to two chunks merged; identical ids and logits."""
+    shape = dict(n_layer=2, dim=4096, n_head=32, ffn=11008, vocab=32000, ctx=640)
+    prompt = vk.prompt_tokens(9, 60, shape["vocab"])
+    monkeypatch.setenv("VKLLM_ATTN_SMALL_MAX", "64")
+    monkeypatch.setenv("VKLLM_ATTN_LONG", "1")
+    ids_a, logits_a = _device_loop(ctx, vk, shape, 7, prompt, 200)
+    monkeypatch.setenv("VKLLM_ATTN_LONG", "0")
+    ids_b, logits_b = _device_loop(ctx, vk, shape, 7, prompt, 200)
     assert ids_a.tolist() == ids_b.tolist()
     assert np.array_equal(logits_a.view(np.uint16), logits_b.view(np.uint16))
 

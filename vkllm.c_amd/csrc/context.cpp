@@ -203,7 +203,7 @@ static const char *kernel_names[KID_COUNT] = {
     "rope",          "softmax",       "ffn_up_and_gate", "update_rows",   "arg_max",       "fused_embed",
     "fused_qkv_rope", "fused_attn_scores", "fused_attn_pv", "fused_o_resid", "fused_gateup", "fused_down_resid",
     "fused_logits",  "fused_argmax",  "fused_rmsnorm",   "fused_gemm",    "fused_rope_kv", "fused_attn_prefill",
-    "fused_swiglu",   "fused_attn_small", "fused_attn_o"};
+    "fused_swiglu",   "fused_attn_small", "fused_attn_o",    "fused_attn_long"};
 
 vkllm_pipeline *pipeline_of(vkllm_context *ctx, KernelId id)
 {

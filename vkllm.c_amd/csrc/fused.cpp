@@ -41,6 +41,7 @@ struct FusedState
     float *att_scores = nullptr, *att_stats = nullptr, *att_part = nullptr;
     uint32_t *att_count = nullptr; // per-head chunk arrivals of the merge, zero between launches
     uint32_t *attn_sync = nullptr; // counters and flags of the attention + projection launch, zero between launches
+    uint32_t *att_long_sync = nullptr; // per-head counters of the one-kernel long-cache attention, zero between launches
     float *gemm_work = nullptr;    // split-K partial tiles of short-prompt prefill GEMMs
     uint32_t att_cmax = 0, att_chunk = 0;
     // decode attention in one kernel up to this many positions, in two kernels beyond (VKLLM_ATTN_SMALL_MAX)
@@ -48,6 +49,9 @@ struct FusedState
     // one-kernel attention and the output projection in one launch (VKLLM_ATTN_O=1; the default is two launches,
     // which measure faster at the 7B widths); cleared when the device cannot hold both parts' workgroups at once
     bool attn_o = false;
+    // long caches in one attention kernel (VKLLM_ATTN_LONG=0: two); cleared when the device cannot hold every chunk
+    // block at once
+    bool attn_long = true;
     // captured single-token steps: [0] with the one-kernel attention, [1] with the two-kernel attention
     hipGraph_t graph[2] = {nullptr, nullptr};
     hipGraphExec_t exec[2] = {nullptr, nullptr};
@@ -125,7 +129,8 @@ void fused_model_release(vkllm_context *ctx, vkllm_models_llama2 *model)
         (void)hipFree(fs->step);
     if (fs->freqs)
         (void)hipFree(fs->freqs);
-    void *att[] = {fs->att_scores, fs->att_stats, fs->att_part, fs->att_count, fs->attn_sync, fs->gemm_work};
+    void *att[] = {fs->att_scores, fs->att_stats, fs->att_part, fs->att_count, fs->attn_sync, fs->att_long_sync,
+                   fs->gemm_work};
     for (void *b : att)
         if (b)
             (void)hipFree(b);
@@ -173,6 +178,8 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         fs->attn_small_max = small < mp->ctx ? small : mp->ctx;
         const char *ao = getenv("VKLLM_ATTN_O");
         fs->attn_o = ao && *ao == '1';
+        const char *al = getenv("VKLLM_ATTN_LONG");
+        fs->attn_long = !(al && *al == '0');
         HIP_TRY(hipMalloc(&fs->att_scores, H * mp->ctx * sizeof(float)));
         HIP_TRY(hipMalloc(&fs->att_stats, H * C * 2 * sizeof(float)));
         HIP_TRY(hipMalloc(&fs->att_part, H * C * mp->hd * sizeof(float)));
@@ -180,6 +187,8 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         HIP_TRY(hipMemset(fs->att_count, 0, H * sizeof(uint32_t)));
         HIP_TRY(hipMalloc(&fs->attn_sync, vk::kAttnSyncWords * sizeof(uint32_t)));
         HIP_TRY(hipMemset(fs->attn_sync, 0, vk::kAttnSyncWords * sizeof(uint32_t)));
+        HIP_TRY(hipMalloc(&fs->att_long_sync, H * vk::kAttnLongStride * sizeof(uint32_t)));
+        HIP_TRY(hipMemset(fs->att_long_sync, 0, H * vk::kAttnLongStride * sizeof(uint32_t)));
         HIP_TRY(hipMalloc(&fs->gemm_work, kGemmWorkElems * sizeof(float)));
     }
     FusedState *fs = mp->fs;
@@ -256,6 +265,7 @@ static hipError_t launch_decode_kernel(vkllm_context *ctx, ModelPriv *mp, Kernel
     case KID_F_ATTN_PV:
     case KID_F_ATTN_SMALL:
     case KID_F_ATTN_O:
+    case KID_F_ATTN_LONG:
     {
         vk::AttnDecodeArgs at{};
         at.q = fs->q;
@@ -274,6 +284,10 @@ static hipError_t launch_decode_kernel(vkllm_context *ctx, ModelPriv *mp, Kernel
         at.chunk = fs->att_chunk;
         at.groups = vk::attn_groups(mp->H, hd, 8);
         at.scale = 1.0f / sqrtf((float)hd);
+        at.long_sync = fs->att_long_sync;
+        at.err = &fs->dio->err;
+        if (kid == KID_F_ATTN_LONG)
+            return vk::launch_attn_long(st, at, cu);
         if (kid == KID_F_ATTN_SMALL)
             return vk::launch_attn_small(st, at, fs->attn_small_max);
         if (kid == KID_F_ATTN_O)
@@ -348,9 +362,21 @@ static vkllm_err_t enqueue_decode(vkllm_context *ctx, ModelPriv *mp, bool small_
         }
         if (!fused_o)
         {
+            bool long_done = false;
+            if (!small_attn && mp->fs->attn_long)
+            {
+                const hipError_t e = timed(ctx, pipeline_of(ctx, KID_F_ATTN_LONG),
+                                           [&]() { return launch_decode_kernel(ctx, mp, KID_F_ATTN_LONG, l); });
+                if (e == hipSuccess)
+                    long_done = true;
+                else if (e == hipErrorInvalidConfiguration) // the chunk blocks do not fit at once: two kernels
+                    mp->fs->attn_long = false;
+                else
+                    return hip_fail(e, "launch_attn_long", __FILE__, __LINE__);
+            }
             if (small_attn)
                 DTRY(ctx, mp, KID_F_ATTN_SMALL, l);
-            else
+            else if (!long_done)
             {
                 DTRY(ctx, mp, KID_F_ATTN_SCORES, l);
                 DTRY(ctx, mp, KID_F_ATTN_PV, l);
@@ -461,6 +487,10 @@ vkllm_err_t fused_plan_run(vkllm_context *ctx, vkllm_graph *graph)
         if (((volatile vk::DecodeIo *)fs->dio)->err)
         {
             log_error("decode step at position %u: a kernel's wait for other workgroups gave up", p->offset);
+            // the launch that gave up may have left counters set: clear them for the next step
+            (void)hipMemset(fs->attn_sync, 0, vk::kAttnSyncWords * sizeof(uint32_t));
+            (void)hipMemset(fs->att_long_sync, 0, (size_t)mp->H * vk::kAttnLongStride * sizeof(uint32_t));
+            (void)hipDeviceSynchronize();
             return VKLLM_ERR_VULKAN;
         }
         if (fs->trace)
@@ -527,6 +557,7 @@ extern "C" vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *ctx, st
     } families[] = {{"fused_embed", KID_F_EMBED},         {"fused_qkv_rope", KID_F_QKV},
                     {"fused_attn_scores", KID_F_ATTN_SCORES}, {"fused_attn_pv", KID_F_ATTN_PV},
                     {"fused_attn_small", KID_F_ATTN_SMALL}, {"fused_attn_o", KID_F_ATTN_O},
+                    {"fused_attn_long", KID_F_ATTN_LONG},
                     {"fused_o_resid", KID_F_O_RESID},     {"fused_gateup", KID_F_GATEUP},
                     {"fused_down_resid", KID_F_DOWN_RESID}, {"fused_logits", KID_F_LOGITS},
                     {"fused_argmax", KID_F_ARGMAX}};

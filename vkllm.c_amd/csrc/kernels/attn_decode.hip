@@ -7,10 +7,11 @@
 //   short caches (one kernel, attn_decode_small_kernel): block (h, g) scores all kv keys of head h itself, reduces
 //     the softmax statistics in the block and forms the probability-weighted sum for its slice of the head's dims.
 //     attn_o_kernel runs the same blocks and the output projection in one launch.
-//   long caches (two kernels over fixed chunks of `chunk` positions): attn_scores_kernel writes fp16-rounded
-//     scores and each chunk's max and sum of exp; attn_pvc_kernel reduces those statistics (identically in every
-//     block of the head), rounds the chunk's probabilities, forms its partial sums, and the last chunk block of a
-//     head to finish adds the partials in chunk order.
+//   long caches (fixed chunks of `chunk` positions): attn_scores_kernel writes fp16-rounded scores and each chunk's
+//     max and sum of exp; attn_pvc_kernel reduces those statistics (identically in every block of the head),
+//     rounds the chunk's probabilities, forms its partial sums, and the last chunk block of a head to finish adds
+//     the partials in chunk order. attn_long_kernel does both in one launch when every chunk block fits on the
+//     device at once.
 // No kernel uses a device-wide fence (on this GPU one writes back a whole L2); kv == hd takes the reference's
 // transposed product p . V^T.
 #include <float.h>
@@ -210,6 +211,175 @@ __global__ __launch_bounds__(256) void attn_pvc_kernel(AttnDecodeArgs a)
     }
     if (tid == 0)
         __hip_atomic_store(a.count + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// long caches, one kernel: block (h, c) does attn_scores_kernel's and attn_pvc_kernel's work for chunk c with the
+// same arithmetic in the same order, so the output is identical. Its K and V rows (one round trip each at head_dim
+// <= 128) are requested together at the start; the scores stay in LDS; the chunk's statistics go out as
+// agent-scope stores and are counted on the head's counter, and the block waits (bounded) until every live chunk
+// of the head has counted before it reduces them. The partial sums are then merged as in attn_pvc_kernel, on the
+// same counter (a second round of arrivals); the merging block clears it. The launcher admits the launch only when
+// every block can be resident at once.
+constexpr uint32_t kLongSpinLimit = 1u << 20;
+
+__global__ __launch_bounds__(256) void attn_long_kernel(AttnDecodeArgs a)
+{
+    extern __shared__ float sm[]; // this chunk's scores
+    __shared__ float rmax[4], rsum[4];
+    __shared__ float pl[1024];
+    __shared__ float part[2048];
+    __shared__ uint32_t arrivals, gave_up;
+    const uint32_t h = blockIdx.x / a.cmax, c = blockIdx.x % a.cmax;
+    const uint32_t kv = a.step->offset + 1;
+    const uint32_t j0 = c * a.chunk;
+    if (j0 >= kv)
+        return;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t n = min(a.chunk, kv - j0), nc = (kv + a.chunk - 1) / a.chunk;
+    uint32_t *const ctr = a.long_sync + (size_t)h * kAttnLongStride;
+    float *const st = a.stats + (size_t)h * a.cmax * 2;
+    const uint16_t *Vh = a.vc + (size_t)h * a.ctx * a.hd;
+
+    // K and V rows of the chunk
+    const KeyLayout k = key_layout<256>(a.q + (size_t)h * a.hd, a.hd);
+    const u32x4 *Kv = (const u32x4 *)(a.kc + ((size_t)h * a.ctx + j0) * a.hd);
+    constexpr int U = 8, UV = 16; // keys and V rows per thread: 256 of each per round trip at head_dim 128
+    u32x4 ka[U], kb[U];
+    load_keys<U>(k, Kv, k.ks, n - 1, ka, kb);
+    const uint32_t vpr = a.hd / 8, lpr = lanes_pow2(vpr), rpp = 256 / lpr;
+    const uint32_t kl = tid % lpr, ks = tid / lpr;
+    const u32x4 *Vv = (const u32x4 *)(Vh + (size_t)j0 * a.hd) + min(kl, vpr - 1);
+    u32x4 vv[UV];
+#pragma unroll
+    for (int t = 0; t < UV; ++t)
+        vv[t] = Vv[(size_t)min(ks + rpp * t, n - 1) * vpr];
+
+    // scores and the chunk's statistics (attn_scores_kernel)
+    score_keys<U>(k, ka, kb, k.ks, n, a.scale, sm);
+    __syncthreads();
+    float mx = -FLT_MAX;
+    for (uint32_t j = tid; j < n; j += 256)
+        mx = fmaxf(mx, sm[j]);
+    mx = block4_max(mx, rmax);
+    float sum = 0.f;
+    for (uint32_t j = tid; j < n; j += 256)
+        sum += expf(sm[j] - mx);
+    sum = block4_sum(sum, rsum);
+    if (tid == 0)
+    {
+        __hip_atomic_store(st + 2 * c, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(st + 2 * c + 1, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t spins = 0, failed = 0;
+        while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < nc)
+        {
+            if (++spins >= kLongSpinLimit)
+            {
+                failed = 1;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        gave_up = failed;
+    }
+    __syncthreads();
+    if (gave_up)
+    {
+        if (tid == 0)
+            __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        return;
+    }
+
+    // the row's statistics, probabilities and this chunk's partial sums (attn_pvc_kernel)
+    const uint32_t ci = min(tid, nc - 1);
+    const float mc_raw = __hip_atomic_load(st + 2 * ci, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float lc_raw = __hip_atomic_load(st + 2 * ci + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float mc = tid < nc ? mc_raw : -FLT_MAX;
+    const float M = block4_max(mc, rmax);
+    const float L = block4_sum(tid < nc ? lc_raw * expf(mc - M) : 0.f, rsum);
+    uint16_t *out = a.out + (size_t)h * a.hd;
+    if (nc == 1 && tid == 0)
+        __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); // no merge round follows
+    if (kv == a.hd)
+    {
+        // the transposed product needs every position: one chunk (the launcher admits chunk >= head_dim)
+        for (uint32_t j = tid; j < kv; j += 256)
+            pl[j] = h2f(f2h(expf(sm[j] - M) / L));
+        __syncthreads();
+        pv_transposed(pl, Vh, out, kv, a.hd, 0, a.hd);
+        return;
+    }
+    for (uint32_t j = tid; j < n; j += 256)
+        pl[j] = h2f(f2h(expf(sm[j] - M) / L));
+    __syncthreads();
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < UV; ++t)
+    {
+        const uint32_t j = ks + rpp * t;
+        const float pj = j < n ? pl[j] : 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+        {
+            acc[2 * e] = fmaf(pj, half_lo(vv[t][e]), acc[2 * e]);
+            acc[2 * e + 1] = fmaf(pj, half_hi(vv[t][e]), acc[2 * e + 1]);
+        }
+    }
+    if (kl < vpr)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            part[ks * a.hd + kl * 8 + e] = acc[e];
+    __syncthreads();
+    float o = 0.f;
+    if (tid < a.hd)
+        for (uint32_t r = 0; r < rpp; ++r)
+            o += part[r * a.hd + tid];
+    if (nc == 1)
+    {
+        if (tid < a.hd)
+            out[tid] = f2h(o);
+        return;
+    }
+    // merge: the second round of arrivals on the head's counter; the last block adds the partials in chunk order
+    float *P = a.part + (size_t)h * a.cmax * a.hd;
+    if (tid < a.hd)
+        __hip_atomic_store(P + (size_t)c * a.hd + tid, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0)
+        arrivals = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (arrivals != 2 * nc - 1)
+        return;
+    const uint32_t ns = 256 / a.hd > 0 ? 256 / a.hd : 1, sg = tid / a.hd, d = tid % a.hd;
+    if (sg < ns)
+    {
+        float total = 0.f;
+        for (uint32_t i0 = sg; i0 < nc; i0 += 8 * ns)
+        {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                v[u] = __hip_atomic_load(P + (size_t)min(i0 + ns * u, nc - 1) * a.hd + d, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                total += i0 + ns * u < nc ? v[u] : 0.f;
+        }
+        part[sg * a.hd + d] = total;
+    }
+    __syncthreads();
+    if (tid < a.hd)
+    {
+        float total = 0.f;
+        for (uint32_t r = 0; r < ns; ++r)
+            total += part[r * a.hd + tid];
+        out[tid] = f2h(total);
+    }
+    if (tid == 0)
+        __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -523,6 +693,31 @@ hipError_t launch_attn_pv(hipStream_t st, const AttnDecodeArgs &a)
         a.cmax > 256 || !a.part || !a.count)
         return hipErrorInvalidValue;
     attn_pvc_kernel<<<a.H * a.cmax, 256, 0, st>>>(a);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_long(hipStream_t st, const AttnDecodeArgs &a, int cu_count)
+{
+    // one round trip of keys and of V rows per block (head_dim <= 128 with chunks of <= 256 positions); the
+    // transposed product (kv == hd) fits one chunk
+    if (!attn_args_ok(a) || a.hd > 128 || a.cmax == 0 || a.chunk == 0 || a.chunk > 256 || a.chunk < a.hd ||
+        (uint64_t)a.chunk * a.cmax < a.ctx || !a.part || !a.stats || !a.long_sync || !a.err)
+        return hipErrorInvalidValue;
+    const size_t lds = (size_t)a.chunk * sizeof(float);
+    static size_t cached_lds = 0;
+    static int per_cu = 0;
+    if (lds != cached_lds)
+    {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_long_kernel, 256, lds) != hipSuccess)
+            n = 0;
+        per_cu = n;
+        cached_lds = lds;
+    }
+    // the blocks of a head wait for each other: all of them must be resident at once
+    if ((uint64_t)a.H * a.cmax > (uint64_t)(cu_count > 0 ? cu_count : 256) * (uint32_t)per_cu)
+        return hipErrorInvalidConfiguration;
+    attn_long_kernel<<<a.H * a.cmax, 256, lds, st>>>(a);
     return hipGetLastError();
 }
 

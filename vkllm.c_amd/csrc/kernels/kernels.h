@@ -113,11 +113,20 @@ struct AttnDecodeArgs
     uint32_t H, hd, ctx, cmax, chunk, groups;
     float scale;
     uint32_t small_max; // one-kernel attention: positions its LDS holds (set by the launchers)
+    // one-kernel long-cache attention: [H * kAttnLongStride] per-head counters, zero before the first launch (the
+    // kernel leaves them zero), and the flag it sets (system scope) when a wait gives up
+    uint32_t *long_sync;
+    uint32_t *err;
 };
+constexpr uint32_t kAttnLongStride = 64;
 // dim slices per head: the largest divisor of hd / 8 up to max_groups with H * groups <= 1024
 uint32_t attn_groups(uint32_t H, uint32_t hd, uint32_t max_groups);
 hipError_t launch_attn_scores(hipStream_t st, const AttnDecodeArgs &a);
 hipError_t launch_attn_pv(hipStream_t st, const AttnDecodeArgs &a);
+// Long caches in one launch: block (h, c) scores its chunk, publishes the chunk's statistics, waits for the other
+// chunks of head h, then forms its partial sums as attn_pv does (identical results). hipErrorInvalidConfiguration
+// when the device cannot hold every chunk block at once (then use attn_scores + attn_pv).
+hipError_t launch_attn_long(hipStream_t st, const AttnDecodeArgs &a, int cu_count);
 // largest kv the one-kernel attention takes for this shape (0: the shape needs the two-kernel path)
 uint32_t attn_small_limit(const AttnDecodeArgs &a);
 // kv <= kv_max <= min(ctx, attn_small_limit); kv_max sizes the LDS

@@ -54,6 +54,7 @@ enum KernelId
     KID_F_SWIGLU,
     KID_F_ATTN_SMALL,
     KID_F_ATTN_O,
+    KID_F_ATTN_LONG,
     KID_COUNT
 };
 
