@@ -38,7 +38,7 @@ sys.path.insert(0, os.path.join(HERE, "vkllm.c_amd"))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 MODEL_SEED, PROMPT_SEED = 0, 1
-ATTN_SMALL_MAX = 1536  # positions up to which the decode attention is one kernel (VKLLM_ATTN_SMALL_MAX)
+ATTN_SMALL_MAX = 1024  # positions up to which the decode attention is the short-cache kernel (VKLLM_ATTN_SMALL_MAX)
 
 SHAPE_7B = dict(n_layer=32, dim=4096, n_head=32, ffn=11008, vocab=32000)
 SHAPE_13B = dict(n_layer=40, dim=5120, n_head=40, ffn=13824, vocab=32000)

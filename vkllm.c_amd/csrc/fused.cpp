@@ -167,7 +167,7 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         fs->att_cmax = (mp->ctx + fs->att_chunk - 1) / fs->att_chunk;
         const size_t H = mp->H, C = fs->att_cmax;
         const char *sm = getenv("VKLLM_ATTN_SMALL_MAX");
-        uint32_t small = sm && *sm ? (uint32_t)strtoul(sm, nullptr, 10) : 1536u;
+        uint32_t small = sm && *sm ? (uint32_t)strtoul(sm, nullptr, 10) : 1024u;
         vk::AttnDecodeArgs shape{};
         shape.H = mp->H;
         shape.hd = mp->hd;
