@@ -166,8 +166,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint16_t *__restrict__ 
 // e % 4][l % 32]. Loads, LDS layout, tile order and split-K as in gemm_kernel.
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-template <int BM, int BN, int EPI, bool SPLIT>
-__global__ __launch_bounds__(256, 1) void gemm32_kernel(const uint16_t *__restrict__ A,
+// PF: K steps whose global loads are in flight at once. With PF 2 the loads run two steps ahead through two register
+// sets (a step's loads are stored to LDS at the end of the following step); a split tile of a short prompt has little
+// MFMA work per step, and one step of loads in flight leaves it waiting on memory latency every step.
+template <int BM, int BN, int EPI, bool SPLIT, int PF = 1>
+__global__ __launch_bounds__(256, PF) void gemm32_kernel(const uint16_t *__restrict__ A,
                                                         const uint16_t *__restrict__ B, uint16_t *C, float *work,
                                                         uint32_t M, uint32_t N, uint32_t K, uint32_t ldc,
                                                         uint32_t split, uint32_t kchunk, uint32_t tiles_m,
@@ -200,33 +203,35 @@ __global__ __launch_bounds__(256, 1) void gemm32_kernel(const uint16_t *__restri
 
     // every K step lies wholly inside [kb, ke) (the launcher admits K ranges of whole 64-wide steps), so the
     // loads need no masks and each step's body is straight-line code for the scheduler
-    u32x4 ra[AV], rb[BV];
-    auto load = [&](uint32_t k0) {
+    u32x4 ra[PF][AV], rb[PF][BV];
+    auto load = [&](auto set_tag, uint32_t k0) {
+        constexpr int S = decltype(set_tag)::value;
 #pragma unroll
         for (int i = 0; i < AV; ++i)
         {
             const uint32_t v = tid + 256 * i, row = min(m0 + v / 8, M - 1);
-            ra[i] = *(const u32x4 *)(A + (size_t)row * K + k0 + (v % 8) * 8);
+            ra[S][i] = *(const u32x4 *)(A + (size_t)row * K + k0 + (v % 8) * 8);
         }
 #pragma unroll
         for (int i = 0; i < BV; ++i)
         {
             const uint32_t v = tid + 256 * i, row = min(n0 + v / 8, N - 1);
-            rb[i] = __builtin_nontemporal_load((const u32x4 *)(B + (size_t)row * K + k0 + (v % 8) * 8));
+            rb[S][i] = __builtin_nontemporal_load((const u32x4 *)(B + (size_t)row * K + k0 + (v % 8) * 8));
         }
     };
-    auto stash = [&](int buf) {
+    auto stash = [&](auto set_tag, int buf) {
+        constexpr int S = decltype(set_tag)::value;
 #pragma unroll
         for (int i = 0; i < AV; ++i)
         {
             const uint32_t v = tid + 256 * i;
-            *(u32x4 *)(As(buf) + (v / 8) * kLdsRow + (v % 8) * 8) = ra[i];
+            *(u32x4 *)(As(buf) + (v / 8) * kLdsRow + (v % 8) * 8) = ra[S][i];
         }
 #pragma unroll
         for (int i = 0; i < BV; ++i)
         {
             const uint32_t v = tid + 256 * i;
-            *(u32x4 *)(Bs(buf) + (v / 8) * kLdsRow + (v % 8) * 8) = rb[i];
+            *(u32x4 *)(Bs(buf) + (v / 8) * kLdsRow + (v % 8) * 8) = rb[S][i];
         }
     };
     f16x8 af[2][TM], bf[2][TN];
@@ -247,25 +252,26 @@ __global__ __launch_bounds__(256, 1) void gemm32_kernel(const uint16_t *__restri
             for (int j = 0; j < TN; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[from][i], bf[from][j], acc[i][j], 0, 0, 0);
     };
-    // One K step from LDS buffer `buf`. With MORE, the next step's global loads are issued during the first slice
-    // and land in the other buffer during the last one. The group barriers lay the instruction stream out as MFMAs
-    // with the operand reads of the next slice, the global loads and the LDS stores threaded between them.
+    // One K step from LDS buffer `buf`. With LD, global loads of step `kload` go to register set LS during the first
+    // slice; with ST, register set SS is stored to the other LDS buffer during the last one. The group barriers lay
+    // the instruction stream out as MFMAs with the operand reads of the next slice, the global loads and the LDS
+    // stores threaded between them.
     constexpr int NMF = TM * TN, NDR = TM + TN, NLD = AV + BV;
     constexpr int LD_PER = (NLD + NMF - 1) / NMF;
-    auto step = [&](auto more_tag, int buf, uint32_t k0) {
-        constexpr bool MORE = decltype(more_tag)::value;
+    auto step = [&](auto ld_tag, auto st_tag, auto ls_tag, auto ss_tag, int buf, uint32_t kload) {
+        constexpr bool LD = decltype(ld_tag)::value, ST = decltype(st_tag)::value;
         frags(buf, 0, 0);
         frags(buf, 1, 1);
-        if constexpr (MORE)
-            load(k0 + kBK);
+        if constexpr (LD)
+            load(ls_tag, kload);
         mfmas(0);
         frags(buf, 2, 0);
         mfmas(1);
         frags(buf, 3, 1);
         mfmas(0);
         mfmas(1);
-        if constexpr (MORE)
-            stash(buf ^ 1);
+        if constexpr (ST)
+            stash(ss_tag, buf ^ 1);
         // slice 0 operands first, then: slice 0 MFMAs with slice 1 reads and the global loads, slices 1 and 2 with
         // the next slice's reads, slice 3 with the LDS stores
         __builtin_amdgcn_sched_group_barrier(0x100, NDR, 0);
@@ -275,7 +281,7 @@ __global__ __launch_bounds__(256, 1) void gemm32_kernel(const uint16_t *__restri
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
             if (i < NDR)
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            if (MORE && i * LD_PER < NLD)
+            if (LD && i * LD_PER < NLD)
                 __builtin_amdgcn_sched_group_barrier(0x020, LD_PER, 0);
         }
 #pragma unroll
@@ -291,24 +297,71 @@ __global__ __launch_bounds__(256, 1) void gemm32_kernel(const uint16_t *__restri
         for (int i = 0; i < NMF; ++i)
         {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            if (MORE && i * LD_PER < NLD)
+            if (ST && i * LD_PER < NLD)
                 __builtin_amdgcn_sched_group_barrier(0x200, LD_PER, 0);
         }
     };
 
-    load(kb);
-    stash(0);
-    __syncthreads();
-    int cur = 0;
-    uint32_t k0 = kb;
-    for (; k0 + kBK < ke; k0 += kBK)
+    using T = std::true_type;
+    using F = std::false_type;
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, PF - 1>;
+    const uint32_t nsteps = (ke - kb) / kBK;
+    if constexpr (PF == 1)
     {
-        step(std::true_type{}, cur, k0);
+        load(S0{}, kb);
+        stash(S0{}, 0);
         __syncthreads();
-        cur ^= 1;
+        int cur = 0;
+        uint32_t k0 = kb;
+        for (; k0 + kBK < ke; k0 += kBK)
+        {
+            step(T{}, T{}, S0{}, S0{}, cur, k0 + kBK);
+            __syncthreads();
+            cur ^= 1;
+        }
+        step(F{}, F{}, S0{}, S0{}, cur, k0);
     }
-    step(std::false_type{}, cur, k0);
+    else
+    {
+        // step s computes from LDS buffer s % 2, loads step s + 2 into register set s % 2 and stores set
+        // (s + 1) % 2 (step s + 1, loaded during step s - 1) into buffer (s + 1) % 2; pairs keep the sets static
+        load(S0{}, kb);
+        load(S1{}, nsteps > 1 ? kb + kBK : kb); // unconditional: storing set 0 then waits for set 0 only
+        stash(S0{}, 0);
+        __syncthreads();
+        uint32_t s = 0;
+        for (; s + 3 < nsteps; s += 2)
+        {
+            step(T{}, T{}, S0{}, S1{}, 0, kb + (s + 2) * kBK);
+            __syncthreads();
+            step(T{}, T{}, S1{}, S0{}, 1, kb + (s + 3) * kBK);
+            __syncthreads();
+        }
+        const uint32_t left = nsteps - s; // 1, 2 or 3 steps, the first from buffer 0
+        if (left == 3)
+        {
+            step(T{}, T{}, S0{}, S1{}, 0, kb + (s + 2) * kBK);
+            __syncthreads();
+            step(F{}, T{}, S1{}, S0{}, 1, 0);
+            __syncthreads();
+            step(F{}, F{}, S0{}, S0{}, 0, 0);
+        }
+        else if (left == 2)
+        {
+            step(F{}, T{}, S0{}, S1{}, 0, 0);
+            __syncthreads();
+            step(F{}, F{}, S1{}, S1{}, 1, 0);
+        }
+        else
+            step(F{}, F{}, S0{}, S0{}, 0, 0);
+    }
 
+    auto elem = [&](int i, int j, int e, uint32_t &m, uint32_t &n) {
+        m = m0 + wm * WM + i * 32 + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
+        n = n0 + wn * WN + j * 32 + lane % 32;
+        return m < M && n < N;
+    };
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -316,9 +369,8 @@ __global__ __launch_bounds__(256, 1) void gemm32_kernel(const uint16_t *__restri
 #pragma unroll
             for (int e = 0; e < 16; ++e)
             {
-                const uint32_t m = m0 + wm * WM + i * 32 + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
-                const uint32_t n = n0 + wn * WN + j * 32 + lane % 32;
-                if (m >= M || n >= N)
+                uint32_t m, n;
+                if (!elem(i, j, e, m, n))
                     continue;
                 if (SPLIT)
                     work[((size_t)blockIdx.y * M + m) * N + n] = acc[i][j][e];
@@ -370,7 +422,7 @@ static hipError_t launch_tile(hipStream_t st, const uint16_t *A, const uint16_t 
     return hipGetLastError();
 }
 
-template <int BM, int BN, int EPI, bool SPLIT>
+template <int BM, int BN, int EPI, bool SPLIT, int PF = 1>
 static hipError_t launch_tile32(hipStream_t st, const uint16_t *A, const uint16_t *B, uint16_t *C, float *work,
                                 uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, uint32_t splits,
                                 uint32_t kchunk)
@@ -379,7 +431,7 @@ static hipError_t launch_tile32(hipStream_t st, const uint16_t *A, const uint16_
     const size_t lds = gemm_lds<BM, BN>();
     if (!attr_set)
     {
-        hipError_t e = hipFuncSetAttribute((const void *)gemm32_kernel<BM, BN, EPI, SPLIT>,
+        hipError_t e = hipFuncSetAttribute((const void *)gemm32_kernel<BM, BN, EPI, SPLIT, PF>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess)
             return e;
@@ -387,8 +439,8 @@ static hipError_t launch_tile32(hipStream_t st, const uint16_t *A, const uint16_
     }
     const uint32_t tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN, total = tm * tn;
     const uint32_t grid = (total + 7) / 8 * 8;
-    gemm32_kernel<BM, BN, EPI, SPLIT><<<dim3(grid, SPLIT ? splits : 1), 256, lds, st>>>(A, B, C, work, M, N, K, ldc,
-                                                                                       split, kchunk, tm, total);
+    gemm32_kernel<BM, BN, EPI, SPLIT, PF><<<dim3(grid, SPLIT ? splits : 1), 256, lds, st>>>(
+        A, B, C, work, M, N, K, ldc, split, kchunk, tm, total);
     return hipGetLastError();
 }
 
@@ -410,7 +462,9 @@ static hipError_t launch_shape32(hipStream_t st, const uint16_t *A, const uint16
 {
     if (splits <= 1)
         return launch_tile32<BM, BN, EPI, false>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
-    hipError_t e = launch_tile32<BM, BN, EPI, true>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk);
+    // split tiles (short prompts): two K steps of loads in flight where the registers allow it
+    constexpr int PF = BM * BN <= 128 * 128 ? 2 : 1;
+    hipError_t e = launch_tile32<BM, BN, EPI, true, PF>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk);
     if (e != hipSuccess)
         return e;
     return launch_reduce<EPI>(st, work, C, M, N, ldc, split, splits);
@@ -442,13 +496,15 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
     if (K % kBK == 0)
     {
         // 32x32x16 kernel: 256 x 256 tiles when they alone give most CUs a tile; else 128 x 128 tiles (two fit a
-        // CU) with K split until about two workgroups per CU run, each split keeping at least 256 of K
+        // CU) with K split until about two workgroups per CU run, or 1.4 for prompts of at most 128 tokens (their
+        // partial tiles cost more than further splits gain), each split keeping at least 256 of K
         const uint64_t t256 = (uint64_t)((M + 255) / 256) * ((N + 255) / 256);
         if (t256 >= (cus * 3) / 4)
             return launch_shape32<256, 256, EPI>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
         const uint64_t tiles = (uint64_t)((M + 127) / 128) * ((N + 127) / 128);
+        const uint64_t per_cu10 = M <= 128 ? 14 : 20; // workgroups per CU, times 10
         uint32_t splits = 1;
-        while (tiles * splits * 2 <= 2 * (uint64_t)cus && K / (splits * 2) >= 256 &&
+        while (tiles * splits * 2 * 10 <= per_cu10 * cus && K / (splits * 2) >= 256 &&
                (size_t)splits * 2 * M * N <= work_elems)
             splits *= 2;
         const uint32_t kchunk = ((K + splits - 1) / splits + kBK - 1) / kBK * kBK;
