@@ -14,7 +14,9 @@
 //                     of each of two 16-key score blocks that it holds)
 // Pass 1 walks all kv positions for M and L (an online sum, rescaled when the row max grows); pass 2 recomputes
 // the same scores (same instructions, same order, so the same fp16 values) for the blocks at or before the last
-// row's position and accumulates P.V.
+// row's position and accumulates P.V. The exponentials are the hardware's (v_exp_f32 on x log2 e) and p multiplies
+// by 1 / L: the softmax arithmetic per score, not the matrix products, bounds the kernel (the reference's shader
+// leaves exp and the division to the implementation's precision as well).
 #include <float.h>
 
 #include "device_common.h"
@@ -22,6 +24,11 @@
 
 namespace vk
 {
+
+__device__ __forceinline__ float pf_exp(float x)
+{
+    return __expf(x);
+}
 
 typedef _Float16 f16x8a __attribute__((ext_vector_type(8)));
 typedef float f32x4a __attribute__((ext_vector_type(4)));
@@ -135,11 +142,11 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 if (jb + 16 * b + 4 * q4 + e <= pos)
-                    add += expf(st[b][e] - mn);
-        l = l * expf(m - mn) + add;
+                    add += pf_exp(st[b][e] - mn);
+        l = l * pf_exp(m - mn) + add;
         m = mn;
     }
-    const float M = m, L = row4_sum(l);
+    const float M = m, L = row4_sum(l), inv_l = 1.0f / L;
 
     // ---- pass 2: probabilities and P.V over the blocks at or before the workgroup's last row
     const uint32_t last = offset + min(row0 + kPfRows, S) - 1;
@@ -220,7 +227,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
             for (int e = 0; e < 4; ++e)
             {
                 const bool live = jb + 16 * b + 4 * q4 + e <= pos;
-                const uint16_t p = f2h(expf(st[b][e] - M) / L);
+                const uint16_t p = f2h(pf_exp(st[b][e] - M) * inv_l);
                 _Float16 f;
                 __builtin_memcpy(&f, &p, 2);
                 ph[b][e] = live ? f : (_Float16)0.f;
