@@ -611,3 +611,17 @@ extern "C" vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *ctx, st
     *total_ns = (uint64_t)((double)ms * 1e6);
     return VKLLM_ERR_OK;
 }
+
+extern "C" vkllm_err_t vkllm_hip_gemm(struct vkllm_context *ctx, int epi, const uint16_t *A, const uint16_t *B,
+                                      uint16_t *C, uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split,
+                                      float *work, uint64_t work_elems)
+{
+    _CHECK_ARGS(ctx && A && B && C && M > 0 && N > 0 && K >= 8 && K % 8 == 0 && ldc >= N);
+    _CHECK_ARGS(epi == vk::GEMM_PLAIN || epi == vk::GEMM_SILU_HI || epi == vk::GEMM_RESID);
+    _CHECK_ARGS(work != nullptr || work_elems == 0);
+    hipStream_t st = ctx->device->stream;
+    KTRY(ctx, KID_F_GEMM,
+         vk::launch_gemm(st, epi, A, B, C, M, N, K, ldc, split, ctx->device->cu_count, work, (size_t)work_elems));
+    HIP_TRY(hipStreamSynchronize(st));
+    return VKLLM_ERR_OK;
+}

@@ -500,7 +500,32 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
         // partial tiles cost more than further splits gain), each split keeping at least 256 of K
         const uint64_t t256 = (uint64_t)((M + 255) / 256) * ((N + 255) / 256);
         if (t256 >= (cus * 3) / 4)
+        {
+            // A last round of 256 x 256 tiles at most half full would leave most CUs idle for a whole tile's time:
+            // its tile columns run as a product of their own with K split over those CUs (partials added in order
+            // by the reduce), the full rounds as before.
+            const uint32_t tm = (M + 255) / 256, tn = (N + 255) / 256;
+            const uint64_t full = t256 / cus, rem = t256 % cus;
+            if (full >= 1 && rem > 0 && rem * 2 <= cus)
+            {
+                const uint32_t tail_cols = (uint32_t)((rem + tm - 1) / tm), n_split = (tn - tail_cols) * 256;
+                const uint32_t tail_n = N - n_split;
+                uint32_t splits = cus / (tm * tail_cols);
+                while (splits > 1 && (K / splits < 4 * kBK || (size_t)splits * M * tail_n > work_elems))
+                    --splits;
+                if (splits >= 2)
+                {
+                    const uint32_t kchunk = ((K + splits - 1) / splits + kBK - 1) / kBK * kBK;
+                    const uint32_t tail_split = split > n_split ? split - n_split : 0;
+                    hipError_t e = launch_shape32<256, 256, EPI>(st, A, B, C, work, M, n_split, K, ldc, split, 1, K);
+                    if (e != hipSuccess)
+                        return e;
+                    return launch_shape32<256, 256, EPI>(st, A, B + (size_t)n_split * K, C + n_split, work, M, tail_n,
+                                                         K, ldc, tail_split, (K + kchunk - 1) / kchunk, kchunk);
+                }
+            }
             return launch_shape32<256, 256, EPI>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
+        }
         const uint64_t tiles = (uint64_t)((M + 127) / 128) * ((N + 127) / 128);
         const uint64_t per_cu10 = M <= 128 ? 14 : 20; // workgroups per CU, times 10
         uint32_t splits = 1;
