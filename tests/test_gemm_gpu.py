@@ -28,6 +28,13 @@ CASES = [
     (1200, 15300, 1024, RESID, 0, True),      # ragged M and N through the tail split, residual epilogue
     (128, 12288, 4096, PLAIN, 0, True),       # 128-token prompt: 128 x 128 tiles, split K, two K steps in flight
     (128, 12288, 4096, PLAIN, 0, False),      # the same without a work buffer: no split
+    # prompts of <= 128 tokens with tiles for most CUs: whole K per tile, four K steps of loads in flight
+    (128, 22016, 4096, SILU_HI, 11008, True),  # 7B gate+up, 128 tokens
+    (128, 22016, 1216, SILU_HI, 11008, True),  # 19 K steps: four groups of four and a tail of three
+    (100, 32000, 512, PLAIN, 0, True),        # logits shape, ragged M
+    (64, 24576, 1024, RESID, 0, True),        # residual epilogue
+    (96, 24576, 128, PLAIN, 0, True),         # two K steps: tail only
+    (96, 24576, 192, PLAIN, 0, True),         # three K steps: tail only
     (512, 4096, 4096, RESID, 0, True),        # 128 x 128 split K with the residual epilogue
     (2048, 4096, 1024, RESID, 0, True),       # 128 x 128 tiles, enough of them that K is not split
     (77, 1000, 256, PLAIN, 0, True),          # ragged, one partial tile row

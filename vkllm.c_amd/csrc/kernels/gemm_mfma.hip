@@ -17,6 +17,7 @@
 // contiguous runs so a run shares its B tiles in one L2. Global loads are unconditional at clamped addresses (a
 // guarded load compiles to a branch and a wait per load).
 #include <type_traits>
+#include <utility>
 
 #include "device_common.h"
 #include "kernels.h"
@@ -166,11 +167,20 @@ __global__ __launch_bounds__(256) void gemm_kernel(const uint16_t *__restrict__ 
 // e % 4][l % 32]. Loads, LDS layout, tile order and split-K as in gemm_kernel.
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// f(integral_constant<int, J>) for J in the sequence, in order
+template <int... J, typename F>
+__device__ __forceinline__ void for_seq(std::integer_sequence<int, J...>, F &&f)
+{
+    (f(std::integral_constant<int, J>{}), ...);
+}
+
 // PF: K steps whose global loads are in flight at once. With PF 2 the loads run two steps ahead through two register
 // sets (a step's loads are stored to LDS at the end of the following step); a split tile of a short prompt has little
-// MFMA work per step, and one step of loads in flight leaves it waiting on memory latency every step.
+// MFMA work per step, and one step of loads in flight leaves it waiting on memory latency every step. PF 4 (four
+// register sets, 128 x 128 tiles only, one workgroup per CU for the registers) keeps the whole K of a short prompt's
+// tile in one workgroup.
 template <int BM, int BN, int EPI, bool SPLIT, int PF = 1>
-__global__ __launch_bounds__(256, PF) void gemm32_kernel(const uint16_t *__restrict__ A,
+__global__ __launch_bounds__(256, (PF > 2 ? 1 : PF)) void gemm32_kernel(const uint16_t *__restrict__ A,
                                                         const uint16_t *__restrict__ B, uint16_t *C, float *work,
                                                         uint32_t M, uint32_t N, uint32_t K, uint32_t ldc,
                                                         uint32_t split, uint32_t kchunk, uint32_t tiles_m,
@@ -321,6 +331,41 @@ __global__ __launch_bounds__(256, PF) void gemm32_kernel(const uint16_t *__restr
             cur ^= 1;
         }
         step(F{}, F{}, S0{}, S0{}, cur, k0);
+    }
+    else if constexpr (PF > 2)
+    {
+        // Step s computes from LDS buffer s % 2 while register sets hold steps s + 1 .. s + PF - 1 in flight: it
+        // loads step s + PF into set s % PF (free since step s went to LDS) and stores set (s + 1) % PF into buffer
+        // (s + 1) % 2. Loads past the last step re-read the last step (L2 hits), so every step is the same code and
+        // the wait before each store covers only the set being stored. Steps run in groups of PF (static set
+        // indices), the last nsteps % PF in a tail of straight-line steps.
+        static_assert(PF % 2 == 0, "PF > 2 must be even (buffer parity follows the set index)");
+        const uint32_t lastk = kb + (nsteps - 1) * kBK;
+        auto kat = [&](uint32_t st) { return st < nsteps ? kb + st * kBK : lastk; };
+        for_seq(std::make_integer_sequence<int, PF>{}, [&](auto j) { load(j, kat(decltype(j)::value)); });
+        stash(S0{}, 0);
+        __syncthreads();
+        uint32_t s = 0;
+        auto run_steps = [&](auto seq) {
+            for_seq(seq, [&](auto j) {
+                constexpr int J = decltype(j)::value;
+                step(T{}, T{}, j, std::integral_constant<int, (J + 1) % PF>{}, J % 2, kat(s + J + PF));
+                __syncthreads();
+            });
+        };
+        for (; s + PF <= nsteps; s += PF)
+            run_steps(std::make_integer_sequence<int, PF>{});
+        const uint32_t left = nsteps - s;
+        if constexpr (PF >= 4)
+        {
+            if (left == 3)
+                run_steps(std::make_integer_sequence<int, 3>{});
+            else if (left == 2)
+                run_steps(std::make_integer_sequence<int, 2>{});
+            else if (left == 1)
+                run_steps(std::make_integer_sequence<int, 1>{});
+        }
+        static_assert(PF <= 4, "tail covers at most 3 steps");
     }
     else
     {
@@ -527,6 +572,10 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
             return launch_shape32<256, 256, EPI>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
         }
         const uint64_t tiles = (uint64_t)((M + 127) / 128) * ((N + 127) / 128);
+        // prompts of at most 128 tokens whose tiles cover two thirds of the CUs or more ([Wu;Wg], logits): the
+        // whole K per tile with four K steps of loads in flight (one workgroup per CU) beats split K and its reduce
+        if (M <= 128 && tiles * 3 >= (uint64_t)cus * 2)
+            return launch_tile32<128, 128, EPI, false, 4>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
         const uint64_t per_cu10 = M <= 128 ? 14 : 20; // workgroups per CU, times 10
         uint32_t splits = 1;
         while (tiles * splits * 2 * 10 <= per_cu10 * cus && K / (splits * 2) >= 256 &&
