@@ -26,6 +26,8 @@ CASES = [
     (1024, 22016, 1024, SILU_HI, 20000, True),  # SiLU split inside the tail columns
     (2048, 27648, 512, SILU_HI, 13824, True),   # 13B gate+up shape, 2048 tokens: three full rounds + tail
     (1200, 15300, 1024, RESID, 0, True),      # ragged M and N through the tail split, residual epilogue
+    (2048, 5120, 512, RESID, 0, True),        # 13B Wo shape: 160 tiles of 256 x 256 beat 2.5 rounds of 128 x 128
+    (1100, 9000, 256, PLAIN, 0, True),        # the same rule, ragged M and N
     (128, 12288, 4096, PLAIN, 0, True),       # 128-token prompt: 128 x 128 tiles, split K, two K steps in flight
     (128, 12288, 4096, PLAIN, 0, False),      # the same without a work buffer: no split
     # prompts of <= 128 tokens with tiles for most CUs: whole K per tile, four K steps of loads in flight

@@ -6,18 +6,22 @@
 // V slice as [N, K] and the product becomes out[n] = fp16(sum_k p_k V[n][k]) (src/core/vkllm_op_matmul.c:14-24).
 //
 // A workgroup of 4 waves takes 64 query rows of one head; wave w owns rows [16 w, 16 w + 16), so every row's
-// statistics stay inside one wave. Key blocks of 64 positions go through LDS (K as [key][dim], V as [dim][key]),
-// shared by the 4 waves. Products use v_mfma_f32_16x16x32_f16 in the transposed orientation:
+// statistics stay inside one wave. Key blocks of 64 positions go through two LDS buffers (K as [key][dim], V as
+// [dim][key]), shared by the 4 waves, with each block's global loads requested two blocks ahead (the kernel is
+// bound by that latency, not by the matrix pipe). Products use v_mfma_f32_16x16x32_f16 in the transposed orientation:
 //   S^T = K . Q^T   (A = a 16-key slice of the K tile, B = the wave's Q rows held in registers)
 //   O^T += V^T . P^T (A = the V tile read as [dim][key], B = the probabilities straight from the S^T
 //                     accumulators: the 32 keys of a K slice are ordered so that lane l's 8 slots are the 4 keys
 //                     of each of two 16-key score blocks that it holds)
 // Pass 1 walks all kv positions for M and L (an online sum, rescaled when the row max grows); pass 2 recomputes
 // the same scores (same instructions, same order, so the same fp16 values) for the blocks at or before the last
-// row's position and accumulates P.V. The exponentials are the hardware's (v_exp_f32 on x log2 e) and p multiplies
-// by 1 / L: the softmax arithmetic per score, not the matrix products, bounds the kernel (the reference's shader
-// leaves exp and the division to the implementation's precision as well).
+// row's position and accumulates P.V. The exponentials are the hardware's (v_exp_f32 on s log2 e - M log2 e) and p
+// multiplies by 1 / L (the reference's shader leaves exp and the division to the implementation's precision as
+// well). The per-score softmax arithmetic costs more issue cycles than the matrix products, so a block wholly in a
+// wave's future only joins the max, and a block wholly in its past skips the masks.
 #include <float.h>
+
+#include <type_traits>
 
 #include "device_common.h"
 #include "kernels.h"
@@ -25,9 +29,11 @@
 namespace vk
 {
 
-__device__ __forceinline__ float pf_exp(float x)
+// exp(s - m) as 2^(s log2 e - m log2 e): one fused multiply-add and the hardware exponential (v_exp_f32)
+constexpr float kLog2e = 1.4426950408889634f;
+__device__ __forceinline__ float pf_exp2(float x)
 {
-    return __expf(x);
+    return __builtin_amdgcn_exp2f(x);
 }
 
 typedef _Float16 f16x8a __attribute__((ext_vector_type(8)));
@@ -60,8 +66,10 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
     constexpr int KV = kPfKeys * HD / 8 / 256; // 16-byte K vectors per thread per block
     constexpr int VP = 32 * (HD / 8) / 256;    // (key pair, dim chunk) items per thread per block
     constexpr int VT = HD * (kPfKeys / 8) / 256; // transposed rule: (row, key chunk) vectors per thread
-    __shared__ __attribute__((aligned(16))) uint16_t Kt[kPfKeys * KROW];
-    __shared__ __attribute__((aligned(16))) uint16_t Vt[HD * VROW];
+    // two buffers each of the K tile ([key][dim]) and the V tile ([dim][key]); K buffers first
+    extern __shared__ __attribute__((aligned(16))) uint16_t pf_lds[];
+    auto Kt = [&](int b) { return pf_lds + b * (kPfKeys * KROW); };
+    auto Vt = [&](int b) { return pf_lds + 2 * kPfKeys * KROW + b * (HD * VROW); };
 
     const uint32_t D = H * HD, h = blockIdx.y;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q4 = lane >> 4, c16 = lane & 15;
@@ -71,6 +79,8 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
     const uint32_t kv = offset + S;
     const bool transposed = kv == HD;
     const uint16_t *Kh = kc + (size_t)h * ctx * HD, *Vh = vc + (size_t)h * ctx * HD;
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
 
     // Q^T operand: column = this lane's row, K slot 8 q4 + i = dim 32 ks + 8 q4 + i
     f16x8a qf[KS];
@@ -78,26 +88,31 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
     for (int ks = 0; ks < KS; ++ks)
         qf[ks] = *(const f16x8a *)(q + (size_t)rowc * D + (size_t)h * HD + ks * 32 + 8 * q4);
 
-    // register prefetch of a block's K rows (clamped to kv - 1: positions past kv are masked, whatever they hold)
-    u32x4 kr[KV];
-    auto load_k = [&](uint32_t jb) {
+    // Blocks stream through two register sets and the two LDS buffers: while block b is computed from buffer
+    // b % 2, set b % 2 loads block b + 2 and set (b + 1) % 2 (block b + 1, requested a block earlier) is stored to
+    // the other buffer, so global loads run two blocks ahead with one barrier per block. Rows are clamped to kv - 1
+    // (positions past kv are masked, whatever they hold).
+    u32x4 kr[2][KV];
+    auto load_k = [&](auto set_tag, uint32_t jb) {
+        constexpr int SI = decltype(set_tag)::value;
 #pragma unroll
         for (int i = 0; i < KV; ++i)
         {
             const uint32_t v = tid + 256 * i, key = v / (HD / 8), ch = v % (HD / 8);
-            kr[i] = *(const u32x4 *)(Kh + (size_t)min(jb + key, kv - 1) * HD + ch * 8);
+            kr[SI][i] = *(const u32x4 *)(Kh + (size_t)min(jb + key, kv - 1) * HD + ch * 8);
         }
     };
-    auto store_k = [&]() {
+    auto store_k = [&](auto set_tag, int buf) {
+        constexpr int SI = decltype(set_tag)::value;
 #pragma unroll
         for (int i = 0; i < KV; ++i)
         {
             const uint32_t v = tid + 256 * i, key = v / (HD / 8), ch = v % (HD / 8);
-            *(u32x4 *)(Kt + key * KROW + ch * 8) = kr[i];
+            *(u32x4 *)(Kt(buf) + key * KROW + ch * 8) = kr[SI][i];
         }
     };
     // S^T of the wave's 16 rows against the block's 64 keys: st[b][e] = score of key 16 b + 4 q4 + e, row c16
-    auto scores = [&](f32x4a *st) {
+    auto scores = [&](int buf, f32x4a *st) {
 #pragma unroll
         for (int b = 0; b < 4; ++b)
         {
@@ -105,7 +120,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
             {
-                const f16x8a a = *(const f16x8a *)(Kt + (16 * b + c16) * KROW + ks * 32 + 8 * q4);
+                const f16x8a a = *(const f16x8a *)(Kt(buf) + (16 * b + c16) * KROW + ks * 32 + 8 * q4);
                 st[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[ks], st[b], 0, 0, 0);
             }
 #pragma unroll
@@ -115,38 +130,78 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
     };
 
     // ---- pass 1: row max over all kv positions, sum of exp over the causal ones
+    // The wave's rows span positions [pos_lo, pos_hi]: a block wholly before pos_lo (and inside kv) needs no masks,
+    // and a block wholly after pos_hi adds nothing to the sums, only to the max.
+    const uint32_t pos_lo = offset + min(row0 + wave * 16, S - 1), pos_hi = offset + min(row0 + wave * 16 + 15, S - 1);
     float m = -FLT_MAX, l = 0.f;
     const uint32_t nb1 = (kv + kPfKeys - 1) / kPfKeys;
-    load_k(0);
-    for (uint32_t blk = 0; blk < nb1; ++blk)
-    {
-        const uint32_t jb = blk * kPfKeys;
-        __syncthreads();
-        store_k();
-        __syncthreads();
-        if (blk + 1 < nb1)
-            load_k(jb + kPfKeys);
+    auto step1 = [&](auto ld, auto cur, auto nxt, int buf, uint32_t jb) {
+        if constexpr (decltype(ld)::value >= 1)
+            load_k(cur, jb + 2 * kPfKeys);
         f32x4a st[4];
-        scores(st);
+        scores(buf, st);
+        const bool inside = jb + kPfKeys <= kv;
         float bm = -FLT_MAX;
 #pragma unroll
         for (int b = 0; b < 4; ++b)
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                if (jb + 16 * b + 4 * q4 + e < kv)
+                if (inside || jb + 16 * b + 4 * q4 + e < kv)
                     bm = fmaxf(bm, st[b][e]);
         const float mn = fmaxf(m, row4_max(bm));
         float add = 0.f;
+        if (jb + kPfKeys <= pos_lo + 1)
+        {
+            const float nm = -mn * kLog2e;
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+            for (int b = 0; b < 4; ++b)
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (jb + 16 * b + 4 * q4 + e <= pos)
-                    add += pf_exp(st[b][e] - mn);
-        l = l * pf_exp(m - mn) + add;
+                for (int e = 0; e < 4; ++e)
+                    add += pf_exp2(fmaf(st[b][e], kLog2e, nm));
+        }
+        else if (jb <= pos_hi)
+        {
+            const float nm = -mn * kLog2e;
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (jb + 16 * b + 4 * q4 + e <= pos)
+                        add += pf_exp2(fmaf(st[b][e], kLog2e, nm));
+        }
+        l = l * pf_exp2((m - mn) * kLog2e) + add;
         m = mn;
+        if constexpr (decltype(ld)::value >= 0)
+        {
+            store_k(nxt, buf ^ 1);
+            __syncthreads();
+        }
+    };
+    // LD: the step requests block + 2 (1), only stores the next block (0), or neither (-1): the last two steps of a
+    // pass request nothing past it, so the next pass does not wait behind loads it never uses
+    using Ld = std::integral_constant<int, 1>;
+    using St = std::integral_constant<int, 0>;
+    using Nn = std::integral_constant<int, -1>;
+    const uint32_t nb1e = (nb1 + 1) & ~1u;
+    load_k(S0{}, 0);
+    load_k(S1{}, kPfKeys);
+    store_k(S0{}, 0);
+    __syncthreads();
+    uint32_t blk = 0;
+    for (; blk + 2 < nb1e; blk += 2)
+    {
+        step1(Ld{}, S0{}, S1{}, 0, blk * kPfKeys);
+        step1(Ld{}, S1{}, S0{}, 1, (blk + 1) * kPfKeys);
     }
-    const float M = m, L = row4_sum(l), inv_l = 1.0f / L;
+    if (blk + 1 < nb1)
+    {
+        step1(St{}, S0{}, S1{}, 0, blk * kPfKeys);
+        step1(Nn{}, S1{}, S0{}, 1, (blk + 1) * kPfKeys);
+    }
+    else
+        step1(Nn{}, S0{}, S1{}, 0, blk * kPfKeys);
+    __syncthreads(); // the last block's LDS reads are done before pass 2 stores into that buffer
+    const float M = m, L = row4_sum(l), inv_l = 1.0f / L, nM = -M * kLog2e;
 
     // ---- pass 2: probabilities and P.V over the blocks at or before the workgroup's last row
     const uint32_t last = offset + min(row0 + kPfRows, S) - 1;
@@ -155,8 +210,9 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
 #pragma unroll
     for (int d = 0; d < DB; ++d)
         o[d] = (f32x4a){0.f, 0.f, 0.f, 0.f};
-    u32x4 va[VP], vb[VP], vt[VT];
-    auto load_v = [&](uint32_t jb) {
+    u32x4 va[2][VP], vb[2][VP], vt[2][VT];
+    auto load_v = [&](auto set_tag, uint32_t jb) {
+        constexpr int SI = decltype(set_tag)::value;
         if (!transposed)
         {
             // keys 2 p and 2 p + 1 of the block, dims [8 ch, 8 ch + 8)
@@ -164,8 +220,8 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
             for (int i = 0; i < VP; ++i)
             {
                 const uint32_t v = tid + 256 * i, p = v % 32, ch = v / 32;
-                va[i] = *(const u32x4 *)(Vh + (size_t)min(jb + 2 * p, kv - 1) * HD + ch * 8);
-                vb[i] = *(const u32x4 *)(Vh + (size_t)min(jb + 2 * p + 1, kv - 1) * HD + ch * 8);
+                va[SI][i] = *(const u32x4 *)(Vh + (size_t)min(jb + 2 * p, kv - 1) * HD + ch * 8);
+                vb[SI][i] = *(const u32x4 *)(Vh + (size_t)min(jb + 2 * p + 1, kv - 1) * HD + ch * 8);
             }
         }
         else
@@ -175,11 +231,12 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
             for (int i = 0; i < VT; ++i)
             {
                 const uint32_t v = tid + 256 * i, n = v / (kPfKeys / 8), c = v % (kPfKeys / 8);
-                vt[i] = *(const u32x4 *)(Vh + (size_t)n * HD + min(jb + 8 * c, (uint32_t)HD - 8));
+                vt[SI][i] = *(const u32x4 *)(Vh + (size_t)n * HD + min(jb + 8 * c, (uint32_t)HD - 8));
             }
         }
     };
-    auto store_v = [&]() {
+    auto store_v = [&](auto set_tag, int buf) {
+        constexpr int SI = decltype(set_tag)::value;
         if (!transposed)
         {
 #pragma unroll
@@ -189,8 +246,10 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                 {
-                    *(uint32_t *)(Vt + (8 * ch + 2 * e) * VROW + 2 * p) = (va[i][e] & 0xffffu) | (vb[i][e] << 16);
-                    *(uint32_t *)(Vt + (8 * ch + 2 * e + 1) * VROW + 2 * p) = (va[i][e] >> 16) | (vb[i][e] & 0xffff0000u);
+                    *(uint32_t *)(Vt(buf) + (8 * ch + 2 * e) * VROW + 2 * p) =
+                        (va[SI][i][e] & 0xffffu) | (vb[SI][i][e] << 16);
+                    *(uint32_t *)(Vt(buf) + (8 * ch + 2 * e + 1) * VROW + 2 * p) =
+                        (va[SI][i][e] >> 16) | (vb[SI][i][e] & 0xffff0000u);
                 }
             }
         }
@@ -200,34 +259,27 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
             for (int i = 0; i < VT; ++i)
             {
                 const uint32_t v = tid + 256 * i, n = v / (kPfKeys / 8), c = v % (kPfKeys / 8);
-                *(u32x4 *)(Vt + n * VROW + 8 * c) = vt[i];
+                *(u32x4 *)(Vt(buf) + n * VROW + 8 * c) = vt[SI][i];
             }
         }
     };
-    load_k(0);
-    load_v(0);
-    for (uint32_t blk = 0; blk < nb2; ++blk)
-    {
-        const uint32_t jb = blk * kPfKeys;
-        __syncthreads();
-        store_k();
-        store_v();
-        __syncthreads();
-        if (blk + 1 < nb2)
+    auto step2 = [&](auto ld, auto cur, auto nxt, int buf, uint32_t jb) {
+        if constexpr (decltype(ld)::value >= 1)
         {
-            load_k(jb + kPfKeys);
-            load_v(jb + kPfKeys);
+            load_k(cur, jb + 2 * kPfKeys);
+            load_v(cur, jb + 2 * kPfKeys);
         }
         f32x4a st[4];
-        scores(st);
+        scores(buf, st);
         _Float16 ph[4][4];
+        const bool full = jb + kPfKeys <= pos_lo + 1;
 #pragma unroll
         for (int b = 0; b < 4; ++b)
 #pragma unroll
             for (int e = 0; e < 4; ++e)
             {
-                const bool live = jb + 16 * b + 4 * q4 + e <= pos;
-                const uint16_t p = f2h(pf_exp(st[b][e] - M) * inv_l);
+                const bool live = full || jb + 16 * b + 4 * q4 + e <= pos;
+                const uint16_t p = f2h(pf_exp2(fmaf(st[b][e], kLog2e, nM)) * inv_l);
                 _Float16 f;
                 __builtin_memcpy(&f, &p, 2);
                 ph[b][e] = live ? f : (_Float16)0.f;
@@ -241,7 +293,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
 #pragma unroll
             for (int d = 0; d < DB; ++d)
             {
-                const uint16_t *vr = Vt + (16 * d + c16) * VROW + 32 * t + 4 * q4;
+                const uint16_t *vr = Vt(buf) + (16 * d + c16) * VROW + 32 * t + 4 * q4;
                 const uint2 lo = *(const uint2 *)vr, hi = *(const uint2 *)(vr + 16);
                 f16x8a a;
                 const u32x4 w = {lo.x, lo.y, hi.x, hi.y};
@@ -249,7 +301,33 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
                 o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, o[d], 0, 0, 0);
             }
         }
+        if constexpr (decltype(ld)::value >= 0)
+        {
+            store_k(nxt, buf ^ 1);
+            store_v(nxt, buf ^ 1);
+            __syncthreads();
+        }
+    };
+    const uint32_t nb2e = (nb2 + 1) & ~1u;
+    load_k(S0{}, 0);
+    load_v(S0{}, 0);
+    load_k(S1{}, kPfKeys);
+    load_v(S1{}, kPfKeys);
+    store_k(S0{}, 0);
+    store_v(S0{}, 0);
+    __syncthreads();
+    for (blk = 0; blk + 2 < nb2e; blk += 2)
+    {
+        step2(Ld{}, S0{}, S1{}, 0, blk * kPfKeys);
+        step2(Ld{}, S1{}, S0{}, 1, (blk + 1) * kPfKeys);
     }
+    if (blk + 1 < nb2)
+    {
+        step2(St{}, S0{}, S1{}, 0, blk * kPfKeys);
+        step2(Nn{}, S1{}, S0{}, 1, (blk + 1) * kPfKeys);
+    }
+    else
+        step2(Nn{}, S0{}, S1{}, 0, blk * kPfKeys);
     // O^T accumulators: o[d][e] = out[row c16][dim 16 d + 4 q4 + e]
     const uint32_t row = row0 + wave * 16 + c16;
     if (row < S)
@@ -262,6 +340,30 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
             *(uint2 *)(orow + 16 * d + 4 * q4) = w;
         }
     }
+}
+
+// LDS of the kernel: two K tiles [key][dim] and two V tiles [dim][key], rows padded by 8 halves
+template <int HD> constexpr size_t pf_lds_bytes()
+{
+    return (size_t)2 * (kPfKeys * (HD + 8) + HD * (kPfKeys + 8)) * sizeof(uint16_t);
+}
+
+template <int HD>
+static hipError_t launch_pf_hd(hipStream_t st, dim3 grid, const uint16_t *q, const uint16_t *kc, const uint16_t *vc,
+                               uint16_t *out, uint32_t offset, uint32_t S, uint32_t H, uint32_t ctx, float scale)
+{
+    static bool attr_set = false; // LDS beyond the default 64 KB needs the attribute, once per kernel
+    constexpr size_t lds = pf_lds_bytes<HD>();
+    if (!attr_set)
+    {
+        hipError_t e = hipFuncSetAttribute((const void *)attn_prefill_mfma_kernel<HD>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess)
+            return e;
+        attr_set = true;
+    }
+    attn_prefill_mfma_kernel<HD><<<grid, 256, lds, st>>>(q, kc, vc, out, offset, S, H, ctx, scale);
+    return hipGetLastError();
 }
 
 bool attn_prefill_mfma_ok(uint32_t hd)
@@ -277,10 +379,8 @@ hipError_t launch_attn_prefill_mfma(hipStream_t st, const uint16_t *q, const uin
         return hipErrorInvalidValue;
     const dim3 grid((S + kPfRows - 1) / kPfRows, H);
     if (hd == 128)
-        attn_prefill_mfma_kernel<128><<<grid, 256, 0, st>>>(q, kc, vc, out, offset, S, H, ctx, scale);
-    else
-        attn_prefill_mfma_kernel<64><<<grid, 256, 0, st>>>(q, kc, vc, out, offset, S, H, ctx, scale);
-    return hipGetLastError();
+        return launch_pf_hd<128>(st, grid, q, kc, vc, out, offset, S, H, ctx, scale);
+    return launch_pf_hd<64>(st, grid, q, kc, vc, out, offset, S, H, ctx, scale);
 }
 
 } // namespace vk

@@ -544,7 +544,10 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
         // CU) with K split until about two workgroups per CU run, or 1.4 for prompts of at most 128 tokens (their
         // partial tiles cost more than further splits gain), each split keeping at least 256 of K
         const uint64_t t256 = (uint64_t)((M + 255) / 256) * ((N + 255) / 256);
-        if (t256 >= (cus * 3) / 4)
+        // also when 128 x 128 tiles would take more rounds: a pair of them on a CU takes about 2/3 of a 256 x 256
+        // tile's time (13B Wo and down at 2048 tokens: 160 tiles, 141 and 395 us against 189 and 514 us)
+        const uint64_t r256 = (t256 + cus - 1) / cus, r128 = (2 * t256 + cus - 1) / cus;
+        if (t256 >= (cus * 3) / 4 || r128 * 2 > r256 * 3)
         {
             // A last round of 256 x 256 tiles at most half full would leave most CUs idle for a whole tile's time:
             // its tile columns run as a product of their own with K split over those CUs (partials added in order
