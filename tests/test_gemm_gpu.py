@@ -6,8 +6,9 @@ src/shaders/vkllm_matmul.comp) through this GEMM: C = A . B^T with fp16 operands
 once to fp16, with the SiLU or residual epilogue fused. The model tests reach it only at the tiny workload's
 sizes; these cases reach the paths that 7B and 13B prompts take: 256 x 256 tiles, the split-K tail of a partial
 last round of those tiles, 128 x 128 tiles with and without split K, the 64-wide fallback tiles (K not a multiple
-of 64), ragged M and N. The bar is the fp16 rounding of an fp32 sum: |C - ref| <= 1e-3 + 2e-3 |ref|, twice
-that for the residual epilogue, which rounds twice.
+of 64), ragged M and N, and the SwiGLU epilogue that reads [Wu; Wg] as interleaved row blocks. The bar is the
+fp16 rounding of an fp32 sum: |C - ref| <= 1e-3 + 2e-3 |ref|, twice that for the residual and SwiGLU epilogues,
+which round twice.
 """
 import ctypes
 
@@ -16,7 +17,7 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-PLAIN, SILU_HI, RESID = 0, 1, 2
+PLAIN, SILU_HI, RESID, SWIGLU = 0, 1, 2, 3
 WORK_ELEMS = 16 << 20  # the fused step's split-K buffer (floats)
 
 # (M, N, K, epi, split, with_work): sizes assume the 256 CUs of an MI355X where a path depends on the CU count
@@ -39,6 +40,12 @@ CASES = [
     (96, 24576, 192, PLAIN, 0, True),         # three K steps: tail only
     (512, 4096, 4096, RESID, 0, True),        # 128 x 128 split K with the residual epilogue
     (2048, 4096, 1024, RESID, 0, True),       # 128 x 128 tiles, enough of them that K is not split
+    # SwiGLU epilogue: B = [Wu; Wg] read as interleaved 32-row blocks, C = fp16(fp16(up) * fp16(silu(gate)))
+    (1024, 22016, 4096, SWIGLU, 11008, True),  # 7B, 1024 tokens: 256 x 256 tiles and the split-K tail
+    (2048, 27648, 512, SWIGLU, 13824, True),  # 13B FFN widths, 2048 tokens
+    (128, 22016, 1216, SWIGLU, 11008, True),  # 128 tokens: whole K per 128 x 128 tile, four steps in flight
+    (128, 12288, 1024, SWIGLU, 6144, True),   # 128 x 128 tiles with split K and the reduce
+    (100, 3072, 512, SWIGLU, 1536, False),    # ragged M, no work buffer
     (77, 1000, 256, PLAIN, 0, True),          # ragged, one partial tile row
     (77, 1000, 1000, PLAIN, 0, True),         # K % 64 != 0: 128 x 64 tiles
     (300, 1000, 1000, SILU_HI, 500, True),    # K % 64 != 0, M > 128
@@ -47,6 +54,11 @@ CASES = [
 
 def reference(a, b, c0, epi, split):
     acc = a.astype(np.float32) @ b.astype(np.float32).T
+    if epi == SWIGLU:
+        # B = [Wu; Wg]: fp16(fp16(up) * fp16(silu(gate))) as the reference's ffn_up_and_gate rounds it
+        up, gate = acc[:, :split], acc[:, split:]
+        sg = (gate / (1.0 + np.exp(-gate))).astype(np.float16).astype(np.float32)
+        return (up.astype(np.float16).astype(np.float32) * sg).astype(np.float16).astype(np.float32)
     if epi == SILU_HI:
         hi = acc[:, split:]
         acc[:, split:] = hi / (1.0 + np.exp(-hi))
@@ -59,6 +71,7 @@ def reference(a, b, c0, epi, split):
 def run_gemm(ctx, vk, a, b, c0, epi, split, with_work):
     M, K = a.shape
     N = b.shape[0]
+    ldc = c0.shape[1]
     ta = ctx.tensor_from(a, name="A")
     tb = ctx.tensor_from(b, name="B")
     tc = ctx.tensor_from(c0, name="C")
@@ -68,10 +81,10 @@ def run_gemm(ctx, vk, a, b, c0, epi, split, with_work):
             ctx.upload(tw, np.zeros(WORK_ELEMS, np.float32))  # allocates the device memory
         dev = [t.contents.data.dev for t in (ta, tb, tc)]
         work = tw.contents.data.dev if tw is not None else None
-        rc = vk.lib().vkllm_hip_gemm(ctx.vp, epi, dev[0], dev[1], dev[2], M, N, K, N, split, work,
+        rc = vk.lib().vkllm_hip_gemm(ctx.vp, epi, dev[0], dev[1], dev[2], M, N, K, ldc, split, work,
                                      WORK_ELEMS if tw is not None else 0)
         vk.check("vkllm_hip_gemm", rc)
-        return ctx.download(tc).reshape(M, N)
+        return ctx.download(tc).reshape(M, ldc)
     finally:
         for t in (ta, tb, tc, tw):
             if t is not None:
@@ -85,11 +98,13 @@ def test_gemm_paths(ctx, vk, case):
     rng = np.random.default_rng(M * 7 + N * 3 + K + epi)
     a = rng.standard_normal((M, K), dtype=np.float32).astype(np.float16)
     b = (rng.standard_normal((N, K), dtype=np.float32) * (1.0 / np.sqrt(K))).astype(np.float16)
-    c0 = rng.standard_normal((M, N), dtype=np.float32).astype(np.float16) if epi == RESID else \
-        np.zeros((M, N), np.float16)
+    width = split if epi == SWIGLU else N
+    c0 = rng.standard_normal((M, width), dtype=np.float32).astype(np.float16) if epi == RESID else \
+        np.zeros((M, width), np.float16)
     got = run_gemm(ctx, vk, a, b, c0, epi, split, with_work).astype(np.float32)
     ref = reference(a, b, c0, epi, split)
-    tol = (1e-3 + 2e-3 * np.abs(ref)) * (2.0 if epi == RESID else 1.0)
+    # the residual and SwiGLU epilogues round twice
+    tol = (1e-3 + 2e-3 * np.abs(ref)) * (2.0 if epi in (RESID, SWIGLU) else 1.0)
     err = np.abs(got - ref)
     bad = err > tol
     assert not bad.any(), (f"{int(bad.sum())} of {bad.size} outside tolerance; worst at "
@@ -114,5 +129,8 @@ def test_gemm_rejects_bad_arguments(ctx, vk):
     p = ctypes.c_void_p(16)  # never dereferenced: the argument checks fail first
     assert L.vkllm_hip_gemm(ctx.vp, PLAIN, p, p, p, 4, 4, 12, 4, 0, None, 0) == vk.ERR_ARGS  # K % 8 != 0
     assert L.vkllm_hip_gemm(ctx.vp, PLAIN, p, p, p, 4, 8, 16, 4, 0, None, 0) == vk.ERR_ARGS  # ldc < N
-    assert L.vkllm_hip_gemm(ctx.vp, 3, p, p, p, 4, 4, 16, 4, 0, None, 0) == vk.ERR_ARGS  # unknown epilogue
+    assert L.vkllm_hip_gemm(ctx.vp, 4, p, p, p, 4, 4, 16, 4, 0, None, 0) == vk.ERR_ARGS  # unknown epilogue
+    assert L.vkllm_hip_gemm(ctx.vp, SWIGLU, p, p, p, 4, 128, 64, 64, 32, None, 0) == vk.ERR_ARGS  # N != 2 split
+    assert L.vkllm_hip_gemm(ctx.vp, SWIGLU, p, p, p, 4, 128, 96, 64, 64, None, 0) == vk.ERR_ARGS  # K % 64 != 0
+    assert L.vkllm_hip_gemm(ctx.vp, SWIGLU, p, p, p, 4, 96, 64, 48, 48, None, 0) == vk.ERR_ARGS  # N % 64 != 0
     assert L.vkllm_hip_gemm(ctx.vp, PLAIN, p, p, p, 4, 4, 16, 4, 0, None, 64) == vk.ERR_ARGS  # work size, no work

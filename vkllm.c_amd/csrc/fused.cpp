@@ -410,9 +410,17 @@ static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S
              vk::launch_attn_prefill(st, fs->q, ly.kc, ly.vc, fs->attn, offset, S, mp->H, hd, mp->ctx, scale));
         KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_RESID, fs->attn, ly.wo, fs->h, S, D, D, D, 0, cu, fs->gemm_work, kGemmWorkElems));
         KTRY(ctx, KID_F_RMSNORM, vk::launch_rmsnorm_rows(st, fs->h, ly.ffn_norm, fs->xn, S, D, mp->eps));
-        KTRY(ctx, KID_F_GEMM,
-             vk::launch_gemm(st, vk::GEMM_SILU_HI, fs->xn, ly.wug, fs->ug, S, 2 * F, D, 2 * F, F, cu, fs->gemm_work, kGemmWorkElems));
-        KTRY(ctx, KID_F_SWIGLU, vk::launch_swiglu(st, fs->ug, fs->act, S, F));
+        // SwiGLU in the product's epilogue where the shape allows it (gate and up rows read as interleaved blocks);
+        // otherwise up and SiLU(gate) are stored side by side and multiplied by a separate kernel
+        if (D % 64 == 0 && F % 32 == 0)
+            KTRY(ctx, KID_F_GEMM,
+                 vk::launch_gemm(st, vk::GEMM_SWIGLU, fs->xn, ly.wug, fs->act, S, 2 * F, D, F, F, cu, fs->gemm_work, kGemmWorkElems));
+        else
+        {
+            KTRY(ctx, KID_F_GEMM,
+                 vk::launch_gemm(st, vk::GEMM_SILU_HI, fs->xn, ly.wug, fs->ug, S, 2 * F, D, 2 * F, F, cu, fs->gemm_work, kGemmWorkElems));
+            KTRY(ctx, KID_F_SWIGLU, vk::launch_swiglu(st, fs->ug, fs->act, S, F));
+        }
         KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_RESID, fs->act, ly.wd, fs->h, S, D, F, D, 0, cu, fs->gemm_work, kGemmWorkElems));
     }
     KTRY(ctx, KID_F_RMSNORM, vk::launch_rmsnorm_rows(st, fs->h, mp->out_norm, fs->xn, S, D, mp->eps));
@@ -616,8 +624,9 @@ extern "C" vkllm_err_t vkllm_hip_gemm(struct vkllm_context *ctx, int epi, const 
                                       uint16_t *C, uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split,
                                       float *work, uint64_t work_elems)
 {
-    _CHECK_ARGS(ctx && A && B && C && M > 0 && N > 0 && K >= 8 && K % 8 == 0 && ldc >= N);
-    _CHECK_ARGS(epi == vk::GEMM_PLAIN || epi == vk::GEMM_SILU_HI || epi == vk::GEMM_RESID);
+    _CHECK_ARGS(ctx && A && B && C && M > 0 && N > 0 && K >= 8 && K % 8 == 0);
+    _CHECK_ARGS(epi == vk::GEMM_PLAIN || epi == vk::GEMM_SILU_HI || epi == vk::GEMM_RESID || epi == vk::GEMM_SWIGLU);
+    _CHECK_ARGS(epi == vk::GEMM_SWIGLU ? (K % 64 == 0 && N % 64 == 0 && split * 2 == N && ldc >= split) : ldc >= N);
     _CHECK_ARGS(work != nullptr || work_elems == 0);
     hipStream_t st = ctx->device->stream;
     KTRY(ctx, KID_F_GEMM,

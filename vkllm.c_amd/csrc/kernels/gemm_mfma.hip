@@ -43,6 +43,25 @@ __device__ __forceinline__ void gemm_store(int epi, uint16_t *C, uint32_t ldc, u
         *c = f2h(h2f(*c) + h2f(f2h(v)));
 }
 
+// GEMM_SWIGLU: product column c of [Wu; Wg] (F rows each, F % 32 == 0) is up row 32 (c / 64) + c % 32 when
+// (c / 32) is even, else gate row F + 32 (c / 64) + c % 32; the output column of up column c is 32 (c / 64) + c % 32
+template <int EPI> __device__ __forceinline__ uint32_t gemm_b_row(uint32_t c, uint32_t F)
+{
+    if constexpr (EPI == GEMM_SWIGLU)
+        return 32 * (c / 64) + c % 32 + ((c / 32) % 2) * F;
+    else
+        return c;
+}
+__device__ __forceinline__ uint32_t swiglu_col(uint32_t c)
+{
+    return 32 * (c / 64) + c % 32;
+}
+// fp16(fp16(up) * fp16(silu(gate))) as the reference's ffn_up_and_gate rounds it
+__device__ __forceinline__ uint16_t swiglu_out(float up, float gate)
+{
+    return f2h(h2f(f2h(up)) * h2f(f2h(silu(gate))));
+}
+
 // SPLIT: workgroup z of gridDim.y covers K columns [z * kchunk, min(K, (z + 1) * kchunk)) and writes its fp32 tile
 // to work[z][M][N] instead of C
 template <int BM, int BN, int EPI, bool SPLIT>
@@ -179,12 +198,15 @@ __device__ __forceinline__ void for_seq(std::integer_sequence<int, J...>, F &&f)
 // MFMA work per step, and one step of loads in flight leaves it waiting on memory latency every step. PF 4 (four
 // register sets, 128 x 128 tiles only, one workgroup per CU for the registers) keeps the whole K of a short prompt's
 // tile in one workgroup.
+// n_base: product column of the kernel's column 0 (B rows and C columns are addressed from it; N counts the
+// kernel's columns). GEMM_SWIGLU reads the product's columns from [Wu; Wg] as interleaved 32-row blocks and
+// `split` holds F.
 template <int BM, int BN, int EPI, bool SPLIT, int PF = 1>
 __global__ __launch_bounds__(256, (PF > 2 ? 1 : PF)) void gemm32_kernel(const uint16_t *__restrict__ A,
                                                         const uint16_t *__restrict__ B, uint16_t *C, float *work,
                                                         uint32_t M, uint32_t N, uint32_t K, uint32_t ldc,
                                                         uint32_t split, uint32_t kchunk, uint32_t tiles_m,
-                                                        uint32_t tiles_total)
+                                                        uint32_t tiles_total, uint32_t n_base)
 {
     constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
     constexpr int AV = BM * kBK / 8 / 256, BV = BN * kBK / 8 / 256; // 16-byte vectors per thread per K step
@@ -214,6 +236,15 @@ __global__ __launch_bounds__(256, (PF > 2 ? 1 : PF)) void gemm32_kernel(const ui
     // every K step lies wholly inside [kb, ke) (the launcher admits K ranges of whole 64-wide steps), so the
     // loads need no masks and each step's body is straight-line code for the scheduler
     u32x4 ra[PF][AV], rb[PF][BV];
+    // element offsets of this thread's B rows (fixed for the tile) at its 16-byte column of a K step; B has fewer
+    // than 2^32 elements (checked by the launcher)
+    uint32_t boff[BV];
+#pragma unroll
+    for (int i = 0; i < BV; ++i)
+    {
+        const uint32_t v = tid + 256 * i;
+        boff[i] = gemm_b_row<EPI>(n_base + min(n0 + v / 8, N - 1), split) * K + (v % 8) * 8;
+    }
     auto load = [&](auto set_tag, uint32_t k0) {
         constexpr int S = decltype(set_tag)::value;
 #pragma unroll
@@ -224,10 +255,7 @@ __global__ __launch_bounds__(256, (PF > 2 ? 1 : PF)) void gemm32_kernel(const ui
         }
 #pragma unroll
         for (int i = 0; i < BV; ++i)
-        {
-            const uint32_t v = tid + 256 * i, row = min(n0 + v / 8, N - 1);
-            rb[S][i] = __builtin_nontemporal_load((const u32x4 *)(B + (size_t)row * K + k0 + (v % 8) * 8));
-        }
+            rb[S][i] = __builtin_nontemporal_load((const u32x4 *)(B + boff[i] + k0));
     };
     auto stash = [&](auto set_tag, int buf) {
         constexpr int S = decltype(set_tag)::value;
@@ -407,6 +435,23 @@ __global__ __launch_bounds__(256, (PF > 2 ? 1 : PF)) void gemm32_kernel(const ui
         n = n0 + wn * WN + j * 32 + lane % 32;
         return m < M && n < N;
     };
+    if constexpr (EPI == GEMM_SWIGLU && !SPLIT)
+    {
+        // 32-column blocks alternate up and gate (WN is a multiple of 64): block j and j + 1 of a lane hold the
+        // up and gate values of one output column
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; j += 2)
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                {
+                    uint32_t m, n;
+                    if (elem(i, j, e, m, n))
+                        C[(size_t)m * ldc + swiglu_col(n_base + n)] = swiglu_out(acc[i][j][e], acc[i][j + 1][e]);
+                }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -420,7 +465,7 @@ __global__ __launch_bounds__(256, (PF > 2 ? 1 : PF)) void gemm32_kernel(const ui
                 if (SPLIT)
                     work[((size_t)blockIdx.y * M + m) * N + n] = acc[i][j][e];
                 else
-                    gemm_store(EPI, C, ldc, m, n, acc[i][j][e], split);
+                    gemm_store(EPI, C, ldc, m, n_base + n, acc[i][j][e], split);
             }
 }
 
@@ -428,15 +473,34 @@ __global__ __launch_bounds__(256, (PF > 2 ? 1 : PF)) void gemm32_kernel(const ui
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float *work, uint16_t *C, uint32_t M,
                                                                  uint32_t N, uint32_t ldc, uint32_t split,
-                                                                 uint32_t splits)
+                                                                 uint32_t splits, uint32_t n_base)
 {
     const uint64_t total = (uint64_t)M * N;
+    if constexpr (EPI == GEMM_SWIGLU)
+    {
+        // one output per (row, up column); N % 64 == 0
+        const uint32_t half = N / 2;
+        const uint64_t outs = (uint64_t)M * half;
+        for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < outs; i += (uint64_t)gridDim.x * 256)
+        {
+            const uint32_t m = (uint32_t)(i / half), f = (uint32_t)(i % half), c = 64 * (f / 32) + f % 32;
+            const size_t at = (size_t)m * N + c;
+            float up = 0.f, gate = 0.f;
+            for (uint32_t z = 0; z < splits; ++z)
+            {
+                up += work[(size_t)z * total + at];
+                gate += work[(size_t)z * total + at + 32];
+            }
+            C[(size_t)m * ldc + swiglu_col(n_base + c)] = swiglu_out(up, gate);
+        }
+        return;
+    }
     for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (uint64_t)gridDim.x * 256)
     {
         float v = 0.f;
         for (uint32_t z = 0; z < splits; ++z)
             v += work[(size_t)z * total + i];
-        gemm_store(EPI, C, ldc, (uint32_t)(i / N), (uint32_t)(i % N), v, split);
+        gemm_store(EPI, C, ldc, (uint32_t)(i / N), n_base + (uint32_t)(i % N), v, split);
     }
 }
 
@@ -470,7 +534,7 @@ static hipError_t launch_tile(hipStream_t st, const uint16_t *A, const uint16_t 
 template <int BM, int BN, int EPI, bool SPLIT, int PF = 1>
 static hipError_t launch_tile32(hipStream_t st, const uint16_t *A, const uint16_t *B, uint16_t *C, float *work,
                                 uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, uint32_t splits,
-                                uint32_t kchunk)
+                                uint32_t kchunk, uint32_t n_base = 0)
 {
     static bool attr_set = false;
     const size_t lds = gemm_lds<BM, BN>();
@@ -485,34 +549,35 @@ static hipError_t launch_tile32(hipStream_t st, const uint16_t *A, const uint16_
     const uint32_t tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN, total = tm * tn;
     const uint32_t grid = (total + 7) / 8 * 8;
     gemm32_kernel<BM, BN, EPI, SPLIT, PF><<<dim3(grid, SPLIT ? splits : 1), 256, lds, st>>>(
-        A, B, C, work, M, N, K, ldc, split, kchunk, tm, total);
+        A, B, C, work, M, N, K, ldc, split, kchunk, tm, total, n_base);
     return hipGetLastError();
 }
 
 template <int EPI>
 static hipError_t launch_reduce(hipStream_t st, const float *work, uint16_t *C, uint32_t M, uint32_t N, uint32_t ldc,
-                                uint32_t split, uint32_t splits)
+                                uint32_t split, uint32_t splits, uint32_t n_base)
 {
     const uint64_t total = (uint64_t)M * N;
     uint32_t grid = (uint32_t)((total + 255) / 256);
     grid = grid > 4096 ? 4096 : grid;
-    gemm_splitk_reduce_kernel<EPI><<<grid, 256, 0, st>>>(work, C, M, N, ldc, split, splits);
+    gemm_splitk_reduce_kernel<EPI><<<grid, 256, 0, st>>>(work, C, M, N, ldc, split, splits, n_base);
     return hipGetLastError();
 }
 
 template <int BM, int BN, int EPI>
 static hipError_t launch_shape32(hipStream_t st, const uint16_t *A, const uint16_t *B, uint16_t *C, float *work,
                                  uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, uint32_t splits,
-                                 uint32_t kchunk)
+                                 uint32_t kchunk, uint32_t n_base = 0)
 {
     if (splits <= 1)
-        return launch_tile32<BM, BN, EPI, false>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
+        return launch_tile32<BM, BN, EPI, false>(st, A, B, C, work, M, N, K, ldc, split, 1, K, n_base);
     // split tiles (short prompts): two K steps of loads in flight where the registers allow it
     constexpr int PF = BM * BN <= 128 * 128 ? 2 : 1;
-    hipError_t e = launch_tile32<BM, BN, EPI, true, PF>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk);
+    hipError_t e =
+        launch_tile32<BM, BN, EPI, true, PF>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk, n_base);
     if (e != hipSuccess)
         return e;
-    return launch_reduce<EPI>(st, work, C, M, N, ldc, split, splits);
+    return launch_reduce<EPI>(st, work, C, M, N, ldc, split, splits, n_base);
 }
 
 template <int BM, int BN, int EPI>
@@ -528,7 +593,7 @@ static hipError_t launch_shape(hipStream_t st, const uint16_t *A, const uint16_t
     const uint64_t total = (uint64_t)M * N;
     uint32_t grid = (uint32_t)((total + 255) / 256);
     grid = grid > 4096 ? 4096 : grid;
-    gemm_splitk_reduce_kernel<EPI><<<grid, 256, 0, st>>>(work, C, M, N, ldc, split, splits);
+    gemm_splitk_reduce_kernel<EPI><<<grid, 256, 0, st>>>(work, C, M, N, ldc, split, splits, 0);
     return hipGetLastError();
 }
 
@@ -538,6 +603,11 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
                                   uint32_t split, int cu_count)
 {
     const uint32_t cus = cu_count > 0 ? (uint32_t)cu_count : 256;
+    if ((uint64_t)N * K >= (1ull << 32)) // B row offsets are 32-bit
+        return hipErrorInvalidValue;
+    if constexpr (EPI == GEMM_SWIGLU)
+        if (K % kBK != 0 || N % 64 != 0 || N != 2 * split)
+            return hipErrorInvalidValue;
     if (K % kBK == 0)
     {
         // 32x32x16 kernel: 256 x 256 tiles when they alone give most CUs a tile; else 128 x 128 tiles (two fit a
@@ -564,12 +634,11 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
                 if (splits >= 2)
                 {
                     const uint32_t kchunk = ((K + splits - 1) / splits + kBK - 1) / kBK * kBK;
-                    const uint32_t tail_split = split > n_split ? split - n_split : 0;
                     hipError_t e = launch_shape32<256, 256, EPI>(st, A, B, C, work, M, n_split, K, ldc, split, 1, K);
                     if (e != hipSuccess)
                         return e;
-                    return launch_shape32<256, 256, EPI>(st, A, B + (size_t)n_split * K, C + n_split, work, M, tail_n,
-                                                         K, ldc, tail_split, (K + kchunk - 1) / kchunk, kchunk);
+                    return launch_shape32<256, 256, EPI>(st, A, B, C, work, M, tail_n, K, ldc, split,
+                                                         (K + kchunk - 1) / kchunk, kchunk, n_split);
                 }
             }
             return launch_shape32<256, 256, EPI>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
@@ -588,22 +657,27 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
         splits = (K + kchunk - 1) / kchunk;
         return launch_shape32<128, 128, EPI>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk);
     }
-    if (M <= 128)
+    if constexpr (EPI == GEMM_SWIGLU)
+        return hipErrorInvalidValue; // checked above: not reached
+    else
     {
-        // weight-streaming regime: a 128-row tile covers all of M so each weight is read once; K is split over
-        // workgroups when N is narrow
-        const uint32_t tiles = (N + 63) / 64;
-        uint32_t splits = 1;
-        while (tiles * splits <= cus && K / (splits * 2) >= 512 && (size_t)splits * 2 * M * N <= work_elems)
-            splits *= 2;
-        const uint32_t kchunk = ((K + splits - 1) / splits + kBK - 1) / kBK * kBK;
-        splits = (K + kchunk - 1) / kchunk;
-        return launch_shape<128, 64, EPI>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk);
+        if (M <= 128)
+        {
+            // weight-streaming regime: a 128-row tile covers all of M so each weight is read once; K is split over
+            // workgroups when N is narrow
+            const uint32_t tiles = (N + 63) / 64;
+            uint32_t splits = 1;
+            while (tiles * splits <= cus && K / (splits * 2) >= 512 && (size_t)splits * 2 * M * N <= work_elems)
+                splits *= 2;
+            const uint32_t kchunk = ((K + splits - 1) / splits + kBK - 1) / kBK * kBK;
+            splits = (K + kchunk - 1) / kchunk;
+            return launch_shape<128, 64, EPI>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk);
+        }
+        const uint64_t big = (uint64_t)((M + 127) / 128) * ((N + 127) / 128);
+        if (big >= cus)
+            return launch_shape<128, 128, EPI>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
+        return launch_shape<128, 64, EPI>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
     }
-    const uint64_t big = (uint64_t)((M + 127) / 128) * ((N + 127) / 128);
-    if (big >= cus)
-        return launch_shape<128, 128, EPI>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
-    return launch_shape<128, 64, EPI>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
 }
 
 hipError_t launch_gemm(hipStream_t st, int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, uint32_t M,
@@ -620,6 +694,8 @@ hipError_t launch_gemm(hipStream_t st, int epi, const uint16_t *A, const uint16_
         return launch_epi_gemm<GEMM_SILU_HI>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count);
     case GEMM_RESID:
         return launch_epi_gemm<GEMM_RESID>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count);
+    case GEMM_SWIGLU:
+        return launch_epi_gemm<GEMM_SWIGLU>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count);
     default:
         return hipErrorInvalidValue;
     }

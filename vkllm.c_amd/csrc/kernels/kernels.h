@@ -172,6 +172,10 @@ enum GemmEpi : int
     GEMM_PLAIN = 0,   // C = fp16(acc)
     GEMM_SILU_HI = 1, // columns >= split: fp16(silu(acc)), others fp16(acc)
     GEMM_RESID = 2,   // C = fp16(C + fp16(acc)) (C holds the residual)
+    // B = [Wu; Wg] (split = F rows each, N = 2F, F % 32 == 0, K % 64 == 0): C[m][f] (f < F, row stride ldc) =
+    // fp16(fp16(A[m] . Wu[f]) * fp16(silu(A[m] . Wg[f]))). The product reads B's rows as interleaved 32-row blocks
+    // of up and gate rows, so both values of an output meet in one lane.
+    GEMM_SWIGLU = 3,
 };
 // C[M, N] (row stride ldc) = A[M, K] . B[N, K]^T, fp16 operands, fp32 accumulation on MFMA. K % 8 == 0.
 // `work` (work_elems floats) holds split-K partial tiles for short prompts; with too little of it K is not split.
