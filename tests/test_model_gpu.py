@@ -212,6 +212,22 @@ def test_attention_and_projection_in_one_launch(ctx, vk, monkeypatch):
     assert np.array_equal(logits_a.view(np.uint16), logits_b.view(np.uint16))
 
 
+@pytest.mark.parametrize("prompt_len", [100, 300, 1030])
+def test_qkv_rope_epilogue_matches_separate_kernel(ctx, vk, monkeypatch, prompt_len):
+    """RoPE and the K/V append in the prompt step's QKV product epilogue against the stored product and the separate
+    RoPE kernel (src/shaders/vkllm_rope.comp, src/shaders/vkllm_update_rows.comp), at the 7B widths: the split-K reduce
+    (100 tokens), 128 x 128 tiles (300) and 256 x 256 tiles with a ragged last row block (1030), then decode steps
+    reading the appended cache; identical ids and logits."""
+    shape = dict(n_layer=2, dim=4096, n_head=32, ffn=11008, vocab=32000, ctx=1100)
+    prompt = vk.prompt_tokens(9, prompt_len, shape["vocab"])
+    monkeypatch.setenv("VKLLM_ROPE_EPI", "1")
+    ids_a, logits_a = _device_loop(ctx, vk, shape, 7, prompt, 4)
+    monkeypatch.setenv("VKLLM_ROPE_EPI", "0")
+    ids_b, logits_b = _device_loop(ctx, vk, shape, 7, prompt, 4)
+    assert ids_a.tolist() == ids_b.tolist()
+    assert np.array_equal(logits_a.view(np.uint16), logits_b.view(np.uint16))
+
+
 def test_long_cache_attention_in_one_launch(ctx, vk, monkeypatch):
     """The long-cache attention in one launch (chunk blocks wait for each other's statistics) against the scores and
     P.V kernels, at the 7B widths with a 640-position cache (3 chunks of 224): from the first long-cache step through

@@ -32,6 +32,7 @@ struct FusedState
     uint16_t *h = nullptr, *xn = nullptr, *qkv = nullptr, *q = nullptr, *attn = nullptr, *act = nullptr,
              *ug = nullptr, *logits = nullptr;
     uint32_t *ids = nullptr, *toks = nullptr;
+    float *rope_cs = nullptr;    // a prompt step's RoPE angles [S][hd / 2][2], shared by its layers
     vk::Step *step = nullptr;    // device
     vk::Step *step_h = nullptr;  // pinned staging for step + first token
     uint32_t *io_h = nullptr;    // pinned: a prefill's ids, uploaded and read back
@@ -52,6 +53,9 @@ struct FusedState
     // long caches in one attention kernel (VKLLM_ATTN_LONG=0: two); cleared when the device cannot hold every chunk
     // block at once
     bool attn_long = true;
+    // prompt steps: RoPE and the K/V append in the QKV product's epilogue where the shape allows it
+    // (VKLLM_ROPE_EPI=0: the stored product and a separate kernel)
+    bool rope_epi = true;
     // captured single-token steps: [0] with the one-kernel attention, [1] with the two-kernel attention
     hipGraph_t graph[2] = {nullptr, nullptr};
     hipGraphExec_t exec[2] = {nullptr, nullptr};
@@ -89,11 +93,13 @@ void fused_plan_free(void *plan)
 
 static void free_buffers(FusedState *fs)
 {
-    void *bufs[] = {fs->h, fs->xn, fs->qkv, fs->q, fs->attn, fs->act, fs->ug, fs->logits, fs->ids, fs->toks};
+    void *bufs[] = {fs->h, fs->xn, fs->qkv, fs->q, fs->attn, fs->act, fs->ug, fs->logits, fs->ids, fs->toks,
+                    fs->rope_cs};
     for (void *b : bufs)
         if (b)
             (void)hipFree(b);
     fs->h = fs->xn = fs->qkv = fs->q = fs->attn = fs->act = fs->ug = fs->logits = nullptr;
+    fs->rope_cs = nullptr;
     fs->ids = fs->toks = nullptr;
     fs->cap_S = 0;
 }
@@ -180,6 +186,8 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         fs->attn_o = ao && *ao == '1';
         const char *al = getenv("VKLLM_ATTN_LONG");
         fs->attn_long = !(al && *al == '0');
+        const char *re = getenv("VKLLM_ROPE_EPI");
+        fs->rope_epi = !(re && *re == '0');
         HIP_TRY(hipMalloc(&fs->att_scores, H * mp->ctx * sizeof(float)));
         HIP_TRY(hipMalloc(&fs->att_stats, H * C * 2 * sizeof(float)));
         HIP_TRY(hipMalloc(&fs->att_part, H * C * mp->hd * sizeof(float)));
@@ -214,6 +222,7 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
     HIP_TRY(hipMalloc(&fs->logits, Sz * V * 2));
     HIP_TRY(hipMalloc(&fs->ids, Sz * 4));
     HIP_TRY(hipMalloc(&fs->toks, Sz * 4));
+    HIP_TRY(hipMalloc(&fs->rope_cs, Sz * mp->hd * sizeof(float)));
     HIP_TRY(hipHostMalloc((void **)&fs->io_h, Sz * 4, hipHostMallocDefault));
     fs->cap_S = S;
     return VKLLM_ERR_OK;
@@ -399,13 +408,26 @@ static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S
     const uint32_t D = mp->D, F = mp->F, V = mp->V, hd = mp->hd;
     const float scale = 1.0f / sqrtf((float)hd);
     KTRY(ctx, KID_F_EMBED, vk::launch_embed_rows(st, fs->toks, S, mp->embd, fs->h, V, D, mp->pad_id));
+    // RoPE in the QKV product's epilogue where the shape allows it (angles computed once for all layers);
+    // otherwise the product is stored and a separate kernel rotates and appends
+    const bool rope_epi = fs->rope_epi && D % 64 == 0 && hd >= 32 && (hd & (hd - 1)) == 0;
+    if (rope_epi)
+        KTRY(ctx, KID_F_ROPE_KV, vk::launch_rope_table(st, fs->rope_cs, fs->freqs, offset, S, hd));
     for (uint32_t l = 0; l < mp->L; ++l)
     {
         const ModelPriv::Layer &ly = mp->layers[l];
         KTRY(ctx, KID_F_RMSNORM, vk::launch_rmsnorm_rows(st, fs->h, ly.attn_norm, fs->xn, S, D, mp->eps));
-        KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_PLAIN, fs->xn, ly.wqkv, fs->qkv, S, 3 * D, D, 3 * D, 0, cu, fs->gemm_work, kGemmWorkElems));
-        KTRY(ctx, KID_F_ROPE_KV,
-             vk::launch_rope_kv(st, fs->qkv, fs->q, ly.kc, ly.vc, fs->freqs, offset, S, D, hd, mp->ctx));
+        if (rope_epi)
+        {
+            const vk::GemmRope rope{fs->q, ly.kc, ly.vc, fs->rope_cs, offset, D, hd, mp->ctx};
+            KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_QKV_ROPE, fs->xn, ly.wqkv, fs->qkv, S, 3 * D, D, 3 * D, 0, cu, fs->gemm_work, kGemmWorkElems, &rope));
+        }
+        else
+        {
+            KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_PLAIN, fs->xn, ly.wqkv, fs->qkv, S, 3 * D, D, 3 * D, 0, cu, fs->gemm_work, kGemmWorkElems));
+            KTRY(ctx, KID_F_ROPE_KV,
+                 vk::launch_rope_kv(st, fs->qkv, fs->q, ly.kc, ly.vc, fs->freqs, offset, S, D, hd, mp->ctx));
+        }
         KTRY(ctx, KID_F_ATTN_PREFILL,
              vk::launch_attn_prefill(st, fs->q, ly.kc, ly.vc, fs->attn, offset, S, mp->H, hd, mp->ctx, scale));
         KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_RESID, fs->attn, ly.wo, fs->h, S, D, D, D, 0, cu, fs->gemm_work, kGemmWorkElems));

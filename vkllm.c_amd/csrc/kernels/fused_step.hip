@@ -809,6 +809,28 @@ hipError_t launch_rope_kv(hipStream_t st, const uint16_t *qkv, uint16_t *q, uint
     return hipGetLastError();
 }
 
+// RoPE angles of a prompt step, once for all layers: the same f = pos / freqs[w] and cosf / sinf as rope_kv_kernel
+__global__ void rope_table_kernel(float *cs, const float *freqs, uint32_t offset, uint32_t S, uint32_t half)
+{
+    const uint64_t total = (uint64_t)S * half;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (uint64_t)gridDim.x * blockDim.x)
+    {
+        const uint32_t s = (uint32_t)(i / half), w = (uint32_t)(i % half);
+        const float f = (float)(offset + s) / freqs[w];
+        cs[2 * i] = cosf(f);
+        cs[2 * i + 1] = sinf(f);
+    }
+}
+
+hipError_t launch_rope_table(hipStream_t st, float *cs, const float *freqs, uint32_t offset, uint32_t S, uint32_t hd)
+{
+    const uint64_t total = (uint64_t)S * (hd / 2);
+    uint32_t grid = (uint32_t)((total + 255) / 256);
+    grid = grid > 4096 ? 4096 : grid;
+    rope_table_kernel<<<grid, 256, 0, st>>>(cs, freqs, offset, S, hd / 2);
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // up * SiLU(gate) (src/models/vkllm_llama2_layers.c:54-60, BIN op 2) on a [S, 2F] block whose gate half already
 // holds fp16(silu(gate))

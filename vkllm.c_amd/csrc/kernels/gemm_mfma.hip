@@ -62,6 +62,47 @@ __device__ __forceinline__ uint16_t swiglu_out(float up, float gate)
     return f2h(h2f(f2h(up)) * h2f(f2h(silu(gate))));
 }
 
+// GEMM_QKV_ROPE: element (m, c) of region `region` (0 q, 1 k, 2 v) at head `head`, head dim `dim`; v is the
+// element's fp16-rounded value and w its RoPE partner's (dim ^ 1), as launch_rope_kv combines them
+__device__ __forceinline__ void rope_store(const GemmRope &r, uint32_t m, uint32_t region, uint32_t c,
+                                           uint32_t head, uint32_t dim, float v, float w)
+{
+    const size_t cache = ((size_t)head * r.ctx + r.offset + m) * r.hd + dim;
+    if (region == 2)
+    {
+        r.vc[cache] = f2h(v);
+        return;
+    }
+    const float *cs = r.cs + ((size_t)m * (r.hd / 2) + dim / 2) * 2;
+    const float out = (dim & 1) == 0 ? rope_mul_sub(cs[0], v, cs[1], w) : rope_mul_add(cs[1], w, cs[0], v);
+    if (region == 0)
+        r.q[(size_t)m * r.D + c] = f2h(out);
+    else
+        r.kc[cache] = f2h(out);
+}
+
+// GEMM_QKV_ROPE: 8 consecutive product columns from `a` (a multiple of 8) of row m, as fp16: four RoPE pairs of q
+// or k rotated and stored, or v stored, as one 16-byte vector each
+__device__ __forceinline__ void rope_store8(const GemmRope &r, uint32_t m, uint32_t a, u32x4 v)
+{
+    const uint32_t region = (a >= r.D) + (a >= 2 * r.D), c = a - region * r.D, head = c / r.hd, dim = c % r.hd;
+    const size_t cache = ((size_t)head * r.ctx + r.offset + m) * r.hd + dim;
+    if (region == 2)
+    {
+        *(u32x4 *)(r.vc + cache) = v;
+        return;
+    }
+    const float *cs = r.cs + ((size_t)m * (r.hd / 2) + dim / 2) * 2;
+    u32x4 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+    {
+        const float x0 = half_lo(v[k]), x1 = half_hi(v[k]), co = cs[2 * k], sn = cs[2 * k + 1];
+        o[k] = pack2(f2h(rope_mul_sub(co, x0, sn, x1)), f2h(rope_mul_add(sn, x0, co, x1)));
+    }
+    *(u32x4 *)(region == 0 ? r.q + (size_t)m * r.D + c : r.kc + cache) = o;
+}
+
 // SPLIT: workgroup z of gridDim.y covers K columns [z * kchunk, min(K, (z + 1) * kchunk)) and writes its fp32 tile
 // to work[z][M][N] instead of C
 template <int BM, int BN, int EPI, bool SPLIT>
@@ -206,7 +247,7 @@ __global__ __launch_bounds__(256, (PF > 2 ? 1 : PF)) void gemm32_kernel(const ui
                                                         const uint16_t *__restrict__ B, uint16_t *C, float *work,
                                                         uint32_t M, uint32_t N, uint32_t K, uint32_t ldc,
                                                         uint32_t split, uint32_t kchunk, uint32_t tiles_m,
-                                                        uint32_t tiles_total, uint32_t n_base)
+                                                        uint32_t tiles_total, uint32_t n_base, GemmRope rope)
 {
     constexpr int WM = BM / 2, WN = BN / 2, TM = WM / 32, TN = WN / 32;
     constexpr int AV = BM * kBK / 8 / 256, BV = BN * kBK / 8 / 256; // 16-byte vectors per thread per K step
@@ -430,26 +471,67 @@ __global__ __launch_bounds__(256, (PF > 2 ? 1 : PF)) void gemm32_kernel(const ui
             step(F{}, F{}, S0{}, S0{}, 0, 0);
     }
 
-    auto elem = [&](int i, int j, int e, uint32_t &m, uint32_t &n) {
-        m = m0 + wm * WM + i * 32 + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
-        n = n0 + wn * WN + j * 32 + lane % 32;
-        return m < M && n < N;
-    };
-    if constexpr (EPI == GEMM_SWIGLU && !SPLIT)
+    if constexpr (!SPLIT)
     {
-        // 32-column blocks alternate up and gate (WN is a multiple of 64): block j and j + 1 of a lane hold the
-        // up and gate values of one output column
+        // Epilogue through LDS (the K-step buffers are free now): each lane writes its fp16 outputs into a row-major
+        // tile, then the workgroup moves 16-byte row chunks to their destinations, so the stores (and the residual's
+        // loads) are whole vectors instead of one 2-byte element per lane. SwiGLU tiles have BN / 2 output columns.
+        constexpr int OC = EPI == GEMM_SWIGLU ? BN / 2 : BN;
+        constexpr int TROW = OC + 8; // halves; rows 4 apart then start 16 banks apart
+        static_assert(BM * TROW <= 2 * (BM + BN) * kLdsRow, "epilogue tile fits the K-step buffers");
+        __syncthreads();
+        uint16_t *T = lds;
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < TN; j += 2)
+            for (int j = 0; j < TN; j += (EPI == GEMM_SWIGLU ? 2 : 1))
 #pragma unroll
                 for (int e = 0; e < 16; ++e)
                 {
-                    uint32_t m, n;
-                    if (elem(i, j, e, m, n))
-                        C[(size_t)m * ldc + swiglu_col(n_base + n)] = swiglu_out(acc[i][j][e], acc[i][j + 1][e]);
+                    const uint32_t rt = wm * WM + i * 32 + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
+                    const uint32_t ct = wn * WN + j * 32 + lane % 32;
+                    if constexpr (EPI == GEMM_SWIGLU)
+                        T[rt * TROW + swiglu_col(ct)] = swiglu_out(acc[i][j][e], acc[i][j + 1][e]);
+                    else if constexpr (EPI == GEMM_SILU_HI)
+                        T[rt * TROW + ct] = f2h(n_base + n0 + ct >= split ? silu(acc[i][j][e]) : acc[i][j][e]);
+                    else
+                        T[rt * TROW + ct] = f2h(acc[i][j][e]);
                 }
+        __syncthreads();
+        constexpr int CH = OC / 8;
+        const uint32_t oc0 = EPI == GEMM_SWIGLU ? (n_base + n0) / 2 : n_base + n0; // output column of tile column 0
+        const uint32_t oce = EPI == GEMM_SWIGLU ? (n_base + N) / 2 : n_base + N;   // end of this launch's columns
+        const bool vec = ((uintptr_t)C % 16 == 0) && ldc % 8 == 0;
+        for (uint32_t idx = tid; idx < (uint32_t)(BM * CH); idx += 256)
+        {
+            const uint32_t rt = idx / CH, m = m0 + rt, col = oc0 + (idx % CH) * 8;
+            if (m >= M || col >= oce)
+                continue;
+            const uint16_t *t = T + rt * TROW + (idx % CH) * 8;
+            if constexpr (EPI == GEMM_QKV_ROPE)
+                rope_store8(rope, m, col, *(const u32x4 *)t); // N is a multiple of 64: whole chunks
+            else
+            {
+                uint16_t *c = C + (size_t)m * ldc + col;
+                const uint32_t cnt = min(8u, oce - col);
+                if (vec && cnt == 8)
+                {
+                    u32x4 v = *(const u32x4 *)t;
+                    if constexpr (EPI == GEMM_RESID)
+                    {
+                        const u32x4 r = *(const u32x4 *)c;
+#pragma unroll
+                        for (int k = 0; k < 4; ++k)
+                            v[k] = pack2(f2h(h2f((uint16_t)r[k]) + half_lo(v[k])),
+                                         f2h(h2f((uint16_t)(r[k] >> 16)) + half_hi(v[k])));
+                    }
+                    *(u32x4 *)c = v;
+                }
+                else
+                    for (uint32_t k = 0; k < cnt; ++k)
+                        c[k] = EPI == GEMM_RESID ? f2h(h2f(c[k]) + h2f(t[k])) : t[k];
+            }
+        }
         return;
     }
 #pragma unroll
@@ -459,13 +541,10 @@ __global__ __launch_bounds__(256, (PF > 2 ? 1 : PF)) void gemm32_kernel(const ui
 #pragma unroll
             for (int e = 0; e < 16; ++e)
             {
-                uint32_t m, n;
-                if (!elem(i, j, e, m, n))
-                    continue;
-                if (SPLIT)
+                const uint32_t m = m0 + wm * WM + i * 32 + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
+                const uint32_t n = n0 + wn * WN + j * 32 + lane % 32;
+                if (m < M && n < N)
                     work[((size_t)blockIdx.y * M + m) * N + n] = acc[i][j][e];
-                else
-                    gemm_store(EPI, C, ldc, m, n_base + n, acc[i][j][e], split);
             }
 }
 
@@ -473,9 +552,32 @@ __global__ __launch_bounds__(256, (PF > 2 ? 1 : PF)) void gemm32_kernel(const ui
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float *work, uint16_t *C, uint32_t M,
                                                                  uint32_t N, uint32_t ldc, uint32_t split,
-                                                                 uint32_t splits, uint32_t n_base)
+                                                                 uint32_t splits, uint32_t n_base, GemmRope rope)
 {
     const uint64_t total = (uint64_t)M * N;
+    if constexpr (EPI == GEMM_QKV_ROPE)
+    {
+        // one RoPE pair (columns 2p, 2p + 1) per step
+        const uint32_t half = N / 2;
+        const uint64_t pairs = (uint64_t)M * half;
+        for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < pairs; i += (uint64_t)gridDim.x * 256)
+        {
+            const uint32_t m = (uint32_t)(i / half), n = 2 * (uint32_t)(i % half);
+            const size_t at = (size_t)m * N + n;
+            float v0 = 0.f, v1 = 0.f;
+            for (uint32_t z = 0; z < splits; ++z)
+            {
+                v0 += work[(size_t)z * total + at];
+                v1 += work[(size_t)z * total + at + 1];
+            }
+            const uint32_t a = n_base + n, region = (a >= rope.D) + (a >= 2 * rope.D), c = a - region * rope.D;
+            const uint32_t head = c / rope.hd, dim = c % rope.hd;
+            const float q0 = h2f(f2h(v0)), q1 = h2f(f2h(v1));
+            rope_store(rope, m, region, c, head, dim, q0, q1);
+            rope_store(rope, m, region, c + 1, head, dim + 1, q1, q0);
+        }
+        return;
+    }
     if constexpr (EPI == GEMM_SWIGLU)
     {
         // one output per (row, up column); N % 64 == 0
@@ -534,7 +636,7 @@ static hipError_t launch_tile(hipStream_t st, const uint16_t *A, const uint16_t 
 template <int BM, int BN, int EPI, bool SPLIT, int PF = 1>
 static hipError_t launch_tile32(hipStream_t st, const uint16_t *A, const uint16_t *B, uint16_t *C, float *work,
                                 uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, uint32_t splits,
-                                uint32_t kchunk, uint32_t n_base = 0)
+                                uint32_t kchunk, uint32_t n_base = 0, const GemmRope *rope = nullptr)
 {
     static bool attr_set = false;
     const size_t lds = gemm_lds<BM, BN>();
@@ -549,35 +651,36 @@ static hipError_t launch_tile32(hipStream_t st, const uint16_t *A, const uint16_
     const uint32_t tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN, total = tm * tn;
     const uint32_t grid = (total + 7) / 8 * 8;
     gemm32_kernel<BM, BN, EPI, SPLIT, PF><<<dim3(grid, SPLIT ? splits : 1), 256, lds, st>>>(
-        A, B, C, work, M, N, K, ldc, split, kchunk, tm, total, n_base);
+        A, B, C, work, M, N, K, ldc, split, kchunk, tm, total, n_base, rope ? *rope : GemmRope{});
     return hipGetLastError();
 }
 
 template <int EPI>
 static hipError_t launch_reduce(hipStream_t st, const float *work, uint16_t *C, uint32_t M, uint32_t N, uint32_t ldc,
-                                uint32_t split, uint32_t splits, uint32_t n_base)
+                                uint32_t split, uint32_t splits, uint32_t n_base, const GemmRope *rope)
 {
     const uint64_t total = (uint64_t)M * N;
     uint32_t grid = (uint32_t)((total + 255) / 256);
     grid = grid > 4096 ? 4096 : grid;
-    gemm_splitk_reduce_kernel<EPI><<<grid, 256, 0, st>>>(work, C, M, N, ldc, split, splits, n_base);
+    gemm_splitk_reduce_kernel<EPI>
+        <<<grid, 256, 0, st>>>(work, C, M, N, ldc, split, splits, n_base, rope ? *rope : GemmRope{});
     return hipGetLastError();
 }
 
 template <int BM, int BN, int EPI>
 static hipError_t launch_shape32(hipStream_t st, const uint16_t *A, const uint16_t *B, uint16_t *C, float *work,
                                  uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, uint32_t splits,
-                                 uint32_t kchunk, uint32_t n_base = 0)
+                                 uint32_t kchunk, uint32_t n_base = 0, const GemmRope *rope = nullptr)
 {
     if (splits <= 1)
-        return launch_tile32<BM, BN, EPI, false>(st, A, B, C, work, M, N, K, ldc, split, 1, K, n_base);
+        return launch_tile32<BM, BN, EPI, false>(st, A, B, C, work, M, N, K, ldc, split, 1, K, n_base, rope);
     // split tiles (short prompts): two K steps of loads in flight where the registers allow it
     constexpr int PF = BM * BN <= 128 * 128 ? 2 : 1;
-    hipError_t e =
-        launch_tile32<BM, BN, EPI, true, PF>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk, n_base);
+    hipError_t e = launch_tile32<BM, BN, EPI, true, PF>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk,
+                                                        n_base, rope);
     if (e != hipSuccess)
         return e;
-    return launch_reduce<EPI>(st, work, C, M, N, ldc, split, splits, n_base);
+    return launch_reduce<EPI>(st, work, C, M, N, ldc, split, splits, n_base, rope);
 }
 
 template <int BM, int BN, int EPI>
@@ -593,16 +696,20 @@ static hipError_t launch_shape(hipStream_t st, const uint16_t *A, const uint16_t
     const uint64_t total = (uint64_t)M * N;
     uint32_t grid = (uint32_t)((total + 255) / 256);
     grid = grid > 4096 ? 4096 : grid;
-    gemm_splitk_reduce_kernel<EPI><<<grid, 256, 0, st>>>(work, C, M, N, ldc, split, splits, 0);
+    gemm_splitk_reduce_kernel<EPI><<<grid, 256, 0, st>>>(work, C, M, N, ldc, split, splits, 0, GemmRope{});
     return hipGetLastError();
 }
 
 template <int EPI>
 static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint16_t *B, uint16_t *C, float *work,
                                   size_t work_elems, uint32_t M, uint32_t N, uint32_t K, uint32_t ldc,
-                                  uint32_t split, int cu_count)
+                                  uint32_t split, int cu_count, const GemmRope *rope)
 {
     const uint32_t cus = cu_count > 0 ? (uint32_t)cu_count : 256;
+    if constexpr (EPI == GEMM_QKV_ROPE)
+        if (!rope || K % kBK != 0 || rope->D % 64 != 0 || rope->hd < 32 || (rope->hd & (rope->hd - 1)) != 0 ||
+            N != 3 * rope->D || !rope->cs)
+            return hipErrorInvalidValue;
     if ((uint64_t)N * K >= (1ull << 32)) // B row offsets are 32-bit
         return hipErrorInvalidValue;
     if constexpr (EPI == GEMM_SWIGLU)
@@ -634,20 +741,21 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
                 if (splits >= 2)
                 {
                     const uint32_t kchunk = ((K + splits - 1) / splits + kBK - 1) / kBK * kBK;
-                    hipError_t e = launch_shape32<256, 256, EPI>(st, A, B, C, work, M, n_split, K, ldc, split, 1, K);
+                    hipError_t e =
+                        launch_shape32<256, 256, EPI>(st, A, B, C, work, M, n_split, K, ldc, split, 1, K, 0, rope);
                     if (e != hipSuccess)
                         return e;
                     return launch_shape32<256, 256, EPI>(st, A, B, C, work, M, tail_n, K, ldc, split,
-                                                         (K + kchunk - 1) / kchunk, kchunk, n_split);
+                                                         (K + kchunk - 1) / kchunk, kchunk, n_split, rope);
                 }
             }
-            return launch_shape32<256, 256, EPI>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
+            return launch_shape32<256, 256, EPI>(st, A, B, C, work, M, N, K, ldc, split, 1, K, 0, rope);
         }
         const uint64_t tiles = (uint64_t)((M + 127) / 128) * ((N + 127) / 128);
         // prompts of at most 128 tokens whose tiles cover two thirds of the CUs or more ([Wu;Wg], logits): the
         // whole K per tile with four K steps of loads in flight (one workgroup per CU) beats split K and its reduce
         if (M <= 128 && tiles * 3 >= (uint64_t)cus * 2)
-            return launch_tile32<128, 128, EPI, false, 4>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
+            return launch_tile32<128, 128, EPI, false, 4>(st, A, B, C, work, M, N, K, ldc, split, 1, K, 0, rope);
         const uint64_t per_cu10 = M <= 128 ? 14 : 20; // workgroups per CU, times 10
         uint32_t splits = 1;
         while (tiles * splits * 2 * 10 <= per_cu10 * cus && K / (splits * 2) >= 256 &&
@@ -655,9 +763,9 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
             splits *= 2;
         const uint32_t kchunk = ((K + splits - 1) / splits + kBK - 1) / kBK * kBK;
         splits = (K + kchunk - 1) / kchunk;
-        return launch_shape32<128, 128, EPI>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk);
+        return launch_shape32<128, 128, EPI>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk, 0, rope);
     }
-    if constexpr (EPI == GEMM_SWIGLU)
+    if constexpr (EPI == GEMM_SWIGLU || EPI == GEMM_QKV_ROPE)
         return hipErrorInvalidValue; // checked above: not reached
     else
     {
@@ -682,20 +790,22 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
 
 hipError_t launch_gemm(hipStream_t st, int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, uint32_t M,
                        uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, int cu_count, float *work,
-                       size_t work_elems)
+                       size_t work_elems, const GemmRope *rope)
 {
     if (K % 8 != 0 || K < 8 || M == 0 || N == 0)
         return hipErrorInvalidValue;
     switch (epi)
     {
     case GEMM_PLAIN:
-        return launch_epi_gemm<GEMM_PLAIN>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count);
+        return launch_epi_gemm<GEMM_PLAIN>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count, nullptr);
     case GEMM_SILU_HI:
-        return launch_epi_gemm<GEMM_SILU_HI>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count);
+        return launch_epi_gemm<GEMM_SILU_HI>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count, nullptr);
     case GEMM_RESID:
-        return launch_epi_gemm<GEMM_RESID>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count);
+        return launch_epi_gemm<GEMM_RESID>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count, nullptr);
     case GEMM_SWIGLU:
-        return launch_epi_gemm<GEMM_SWIGLU>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count);
+        return launch_epi_gemm<GEMM_SWIGLU>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count, nullptr);
+    case GEMM_QKV_ROPE:
+        return launch_epi_gemm<GEMM_QKV_ROPE>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count, rope);
     default:
         return hipErrorInvalidValue;
     }

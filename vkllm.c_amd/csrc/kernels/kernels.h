@@ -176,12 +176,28 @@ enum GemmEpi : int
     // fp16(fp16(A[m] . Wu[f]) * fp16(silu(A[m] . Wg[f]))). The product reads B's rows as interleaved 32-row blocks
     // of up and gate rows, so both values of an output meet in one lane.
     GEMM_SWIGLU = 3,
+    // B = [Wq; Wk; Wv] (N = 3D, D % 64 == 0, K % 64 == 0, head size a power of two >= 32): the product's row m
+    // (position rope.offset + m) goes out
+    // as the prompt step's q, k and v: q and k rotated by RoPE (each element first rounded to fp16, then the
+    // rotation of launch_rope_kv), q -> rope.q[m][c], k and v -> the caches at that position; C is not written
+    GEMM_QKV_ROPE = 4,
+};
+struct GemmRope
+{
+    uint16_t *q;         // [M, D]
+    uint16_t *kc, *vc;   // layer caches [H, ctx, hd]
+    const float *cs;     // [M][hd / 2][2]: cos and sin of (offset + m) / base^(2w/hd), from launch_rope_table
+    uint32_t offset, D, hd, ctx;
 };
 // C[M, N] (row stride ldc) = A[M, K] . B[N, K]^T, fp16 operands, fp32 accumulation on MFMA. K % 8 == 0.
 // `work` (work_elems floats) holds split-K partial tiles for short prompts; with too little of it K is not split.
+// `rope` is read by GEMM_QKV_ROPE only.
 hipError_t launch_gemm(hipStream_t st, int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, uint32_t M,
                        uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, int cu_count, float *work,
-                       size_t work_elems);
+                       size_t work_elems, const GemmRope *rope = nullptr);
+// cs[s][w] = (cos f, sin f) with f = (offset + s) / freqs[w], s < S, w < hd / 2 (the angles launch_rope_kv uses)
+hipError_t launch_rope_table(hipStream_t st, float *cs, const float *freqs, uint32_t offset, uint32_t S,
+                             uint32_t hd);
 
 // ---- synthetic weights: dst[i] = fp16(normal(stream, i) * std), i < count ----
 hipError_t launch_random_f16(hipStream_t st, uint16_t *dst, uint64_t count, uint64_t stream_key, float std);
