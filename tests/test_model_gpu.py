@@ -228,6 +228,21 @@ def test_qkv_rope_epilogue_matches_separate_kernel(ctx, vk, monkeypatch, prompt_
     assert np.array_equal(logits_a.view(np.uint16), logits_b.view(np.uint16))
 
 
+@pytest.mark.parametrize("prompt_len", [20, 100])
+def test_norm_in_split_k_reduce_matches_separate_pass(ctx, vk, monkeypatch, prompt_len):
+    """The residual add and the next RMSNorm in one pass over the split-K partials of Wo and Wd (prompts of at most
+    128 tokens split K) against the reduce followed by the separate RMSNorm, at the 7B widths: identical ids and
+    logits."""
+    shape = dict(n_layer=2, dim=4096, n_head=32, ffn=11008, vocab=32000, ctx=160)
+    prompt = vk.prompt_tokens(10, prompt_len, shape["vocab"])
+    monkeypatch.setenv("VKLLM_NORM_EPI", "1")
+    ids_a, logits_a = _device_loop(ctx, vk, shape, 7, prompt, 4)
+    monkeypatch.setenv("VKLLM_NORM_EPI", "0")
+    ids_b, logits_b = _device_loop(ctx, vk, shape, 7, prompt, 4)
+    assert ids_a.tolist() == ids_b.tolist()
+    assert np.array_equal(logits_a.view(np.uint16), logits_b.view(np.uint16))
+
+
 def test_long_cache_attention_in_one_launch(ctx, vk, monkeypatch):
     """The long-cache attention in one launch (chunk blocks wait for each other's statistics) against the scores and
     P.V kernels, at the 7B widths with a 640-position cache (3 chunks of 224): from the first long-cache step through

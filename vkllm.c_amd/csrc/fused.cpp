@@ -56,6 +56,8 @@ struct FusedState
     // prompt steps: RoPE and the K/V append in the QKV product's epilogue where the shape allows it
     // (VKLLM_ROPE_EPI=0: the stored product and a separate kernel)
     bool rope_epi = true;
+    // prompt steps: the RMSNorm after each residual product in its split-K reduce (VKLLM_NORM_EPI=0: a separate pass)
+    bool norm_epi = true;
     // captured single-token steps: [0] with the one-kernel attention, [1] with the two-kernel attention
     hipGraph_t graph[2] = {nullptr, nullptr};
     hipGraphExec_t exec[2] = {nullptr, nullptr};
@@ -188,6 +190,8 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         fs->attn_long = !(al && *al == '0');
         const char *re = getenv("VKLLM_ROPE_EPI");
         fs->rope_epi = !(re && *re == '0');
+        const char *ne = getenv("VKLLM_NORM_EPI");
+        fs->norm_epi = !(ne && *ne == '0');
         HIP_TRY(hipMalloc(&fs->att_scores, H * mp->ctx * sizeof(float)));
         HIP_TRY(hipMalloc(&fs->att_stats, H * C * 2 * sizeof(float)));
         HIP_TRY(hipMalloc(&fs->att_part, H * C * mp->hd * sizeof(float)));
@@ -413,10 +417,12 @@ static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S
     const bool rope_epi = fs->rope_epi && D % 64 == 0 && hd >= 32 && (hd & (hd - 1)) == 0;
     if (rope_epi)
         KTRY(ctx, KID_F_ROPE_KV, vk::launch_rope_table(st, fs->rope_cs, fs->freqs, offset, S, hd));
+    // every residual product also leaves the next RMSNorm of the residual stream in xn (in the split-K reduce when
+    // K is split, else as a separate pass)
+    KTRY(ctx, KID_F_RMSNORM, vk::launch_rmsnorm_rows(st, fs->h, mp->layers[0].attn_norm, fs->xn, S, D, mp->eps));
     for (uint32_t l = 0; l < mp->L; ++l)
     {
         const ModelPriv::Layer &ly = mp->layers[l];
-        KTRY(ctx, KID_F_RMSNORM, vk::launch_rmsnorm_rows(st, fs->h, ly.attn_norm, fs->xn, S, D, mp->eps));
         if (rope_epi)
         {
             const vk::GemmRope rope{fs->q, ly.kc, ly.vc, fs->rope_cs, offset, D, hd, mp->ctx};
@@ -430,8 +436,10 @@ static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S
         }
         KTRY(ctx, KID_F_ATTN_PREFILL,
              vk::launch_attn_prefill(st, fs->q, ly.kc, ly.vc, fs->attn, offset, S, mp->H, hd, mp->ctx, scale));
-        KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_RESID, fs->attn, ly.wo, fs->h, S, D, D, D, 0, cu, fs->gemm_work, kGemmWorkElems));
-        KTRY(ctx, KID_F_RMSNORM, vk::launch_rmsnorm_rows(st, fs->h, ly.ffn_norm, fs->xn, S, D, mp->eps));
+        const vk::GemmNorm ffn_norm{ly.ffn_norm, fs->xn, mp->eps};
+        KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_RESID, fs->attn, ly.wo, fs->h, S, D, D, D, 0, cu, fs->gemm_work, kGemmWorkElems, nullptr, fs->norm_epi ? &ffn_norm : nullptr));
+        if (!fs->norm_epi)
+            KTRY(ctx, KID_F_RMSNORM, vk::launch_rmsnorm_rows(st, fs->h, ly.ffn_norm, fs->xn, S, D, mp->eps));
         // SwiGLU in the product's epilogue where the shape allows it (gate and up rows read as interleaved blocks);
         // otherwise up and SiLU(gate) are stored side by side and multiplied by a separate kernel
         if (D % 64 == 0 && F % 32 == 0)
@@ -443,9 +451,11 @@ static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S
                  vk::launch_gemm(st, vk::GEMM_SILU_HI, fs->xn, ly.wug, fs->ug, S, 2 * F, D, 2 * F, F, cu, fs->gemm_work, kGemmWorkElems));
             KTRY(ctx, KID_F_SWIGLU, vk::launch_swiglu(st, fs->ug, fs->act, S, F));
         }
-        KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_RESID, fs->act, ly.wd, fs->h, S, D, F, D, 0, cu, fs->gemm_work, kGemmWorkElems));
+        const vk::GemmNorm next_norm{l + 1 < mp->L ? mp->layers[l + 1].attn_norm : mp->out_norm, fs->xn, mp->eps};
+        KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_RESID, fs->act, ly.wd, fs->h, S, D, F, D, 0, cu, fs->gemm_work, kGemmWorkElems, nullptr, fs->norm_epi ? &next_norm : nullptr));
+        if (!fs->norm_epi)
+            KTRY(ctx, KID_F_RMSNORM, vk::launch_rmsnorm_rows(st, fs->h, next_norm.w, fs->xn, S, D, mp->eps));
     }
-    KTRY(ctx, KID_F_RMSNORM, vk::launch_rmsnorm_rows(st, fs->h, mp->out_norm, fs->xn, S, D, mp->eps));
     KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_PLAIN, fs->xn, mp->out_w, fs->logits, S, V, D, V, 0, cu, fs->gemm_work, kGemmWorkElems));
     KTRY(ctx, KID_F_ARGMAX, vk::launch_argmax_rows(st, fs->logits, fs->ids, S, V));
     return VKLLM_ERR_OK;

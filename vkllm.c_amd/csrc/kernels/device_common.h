@@ -178,6 +178,43 @@ __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi)
     return (uint32_t)lo | ((uint32_t)hi << 16);
 }
 
+// normalises row `x` (D fp16) into `dst` (8 halfs per u32x4); all threads of the block take part
+__device__ __forceinline__ void rmsnorm_row_to(const uint16_t *x, const float *w, u32x4 *dst, uint32_t D, float eps,
+                                               float *red)
+{
+    const uint32_t nv = D / 8;
+    const u32x4 *xv = (const u32x4 *)x;
+    float ss = 0.f;
+    for (uint32_t i = threadIdx.x; i < nv; i += blockDim.x)
+    {
+        u32x4 v = xv[i];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+        {
+            float a = half_lo(v[k]), b = half_hi(v[k]);
+            ss += a * a;
+            ss += b * b;
+        }
+    }
+    ss = block_sum(ss, red);
+    const float alpha = 1.0f / sqrtf(ss / (float)D + eps);
+    const float4 *wv = (const float4 *)w;
+    for (uint32_t i = threadIdx.x; i < nv; i += blockDim.x)
+    {
+        u32x4 v = xv[i];
+        float4 w0 = wv[2 * i], w1 = wv[2 * i + 1];
+        float ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        u32x4 o;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+        {
+            float a = half_lo(v[k]), b = half_hi(v[k]);
+            o[k] = pack2(f2h((a * ws[2 * k]) * alpha), f2h((b * ws[2 * k + 1]) * alpha));
+        }
+        dst[i] = o;
+    }
+}
+
 // wave64 sum with DPP: row reductions (quad_perm, half-row and row mirrors), then row_bcast15/31 fold the four
 // rows into lane 63, which is broadcast with readlane.
 template <int ctrl, int row_mask> __device__ __forceinline__ float dpp_add(float v)

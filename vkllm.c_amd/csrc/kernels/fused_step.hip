@@ -87,44 +87,8 @@ hipError_t launch_embed_decode(hipStream_t st, const DecodeIo *io, Step *step, c
 // ---------------------------------------------------------------------------------------------------------------
 // RMSNORM (src/shaders/vkllm_rmsnorm.comp:31-82): y = fp16((x * w) * (1 / sqrt(sum(x^2) / D + eps)))
 
-// normalises row `x` (D fp16) into `dst` (8 halfs per u32x4); all threads of the block take part
-__device__ __forceinline__ void rmsnorm_row_to(const uint16_t *x, const float *w, u32x4 *dst, uint32_t D, float eps,
-                                               float *red)
-{
-    const uint32_t nv = D / 8;
-    const u32x4 *xv = (const u32x4 *)x;
-    float ss = 0.f;
-    for (uint32_t i = threadIdx.x; i < nv; i += blockDim.x)
-    {
-        u32x4 v = xv[i];
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-        {
-            float a = half_lo(v[k]), b = half_hi(v[k]);
-            ss += a * a;
-            ss += b * b;
-        }
-    }
-    ss = block_sum(ss, red);
-    const float alpha = 1.0f / sqrtf(ss / (float)D + eps);
-    const float4 *wv = (const float4 *)w;
-    for (uint32_t i = threadIdx.x; i < nv; i += blockDim.x)
-    {
-        u32x4 v = xv[i];
-        float4 w0 = wv[2 * i], w1 = wv[2 * i + 1];
-        float ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-        u32x4 o;
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-        {
-            float a = half_lo(v[k]), b = half_hi(v[k]);
-            o[k] = pack2(f2h((a * ws[2 * k]) * alpha), f2h((b * ws[2 * k + 1]) * alpha));
-        }
-        dst[i] = o;
-    }
-}
-
-__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const uint16_t *x, const float *w, uint16_t *y, uint32_t D,
+// 512 threads a row, the block size of the norm fused into the residual products' split-K reduce (same sum order)
+__global__ __launch_bounds__(512) void rmsnorm_rows_kernel(const uint16_t *x, const float *w, uint16_t *y, uint32_t D,
                                                            float eps)
 {
     __shared__ float red[8];
@@ -135,7 +99,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const uint16_t *x, co
 hipError_t launch_rmsnorm_rows(hipStream_t st, const uint16_t *x, const float *w, uint16_t *y, uint32_t S,
                                uint32_t D, float eps)
 {
-    rmsnorm_rows_kernel<<<S, 256, 0, st>>>(x, w, y, D, eps);
+    rmsnorm_rows_kernel<<<S, 512, 0, st>>>(x, w, y, D, eps);
     return hipGetLastError();
 }
 

@@ -606,6 +606,45 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float *wo
     }
 }
 
+// Split-K residual products followed by RMSNorm (every residual product of the token step is): one workgroup per
+// row m, C[m] = fp16(C[m] + fp16(sum over z of work[z][m])) with the splits added in order (as the reduce kernel),
+// then y[m] = RMSNorm(C[m]) * w as rmsnorm_row_to computes it, with launch_rmsnorm_rows's block size (so the same
+// sum order). Each thread re-reads only the vectors it wrote.
+__global__ __launch_bounds__(512) void gemm_resid_norm_kernel(const float *work, uint16_t *C, uint32_t M, uint32_t N,
+                                                              uint32_t splits, const float *w, uint16_t *y,
+                                                              float eps)
+{
+    __shared__ float red[8];
+    const uint32_t m = blockIdx.x, nv = N / 8;
+    const size_t total = (size_t)M * N;
+    u32x4 *cv = (u32x4 *)(C + (size_t)m * N);
+    for (uint32_t i = threadIdx.x; i < nv; i += blockDim.x)
+    {
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+        for (uint32_t z = 0; z < splits; ++z)
+        {
+            const float4 *p = (const float4 *)(work + z * total + (size_t)m * N + 8 * i);
+            const float4 a = p[0], b = p[1];
+            acc[0] += a.x;
+            acc[1] += a.y;
+            acc[2] += a.z;
+            acc[3] += a.w;
+            acc[4] += b.x;
+            acc[5] += b.y;
+            acc[6] += b.z;
+            acc[7] += b.w;
+        }
+        const u32x4 r = cv[i];
+        u32x4 o;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            o[k] = pack2(f2h(half_lo(r[k]) + h2f(f2h(acc[2 * k]))), f2h(half_hi(r[k]) + h2f(f2h(acc[2 * k + 1]))));
+        cv[i] = o;
+    }
+    rmsnorm_row_to(C + (size_t)m * N, w, (u32x4 *)(y + (size_t)m * N), N, eps, red);
+}
+
 template <int BM, int BN> static size_t gemm_lds()
 {
     return (size_t)2 * (BM + BN) * kLdsRow * sizeof(uint16_t);
@@ -703,7 +742,8 @@ static hipError_t launch_shape(hipStream_t st, const uint16_t *A, const uint16_t
 template <int EPI>
 static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint16_t *B, uint16_t *C, float *work,
                                   size_t work_elems, uint32_t M, uint32_t N, uint32_t K, uint32_t ldc,
-                                  uint32_t split, int cu_count, const GemmRope *rope)
+                                  uint32_t split, int cu_count, const GemmRope *rope, const GemmNorm *norm,
+                                  bool *normed)
 {
     const uint32_t cus = cu_count > 0 ? (uint32_t)cu_count : 256;
     if constexpr (EPI == GEMM_QKV_ROPE)
@@ -763,6 +803,19 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
             splits *= 2;
         const uint32_t kchunk = ((K + splits - 1) / splits + kBK - 1) / kBK * kBK;
         splits = (K + kchunk - 1) / kchunk;
+        if constexpr (EPI == GEMM_RESID)
+            if (norm && splits > 1)
+            {
+                // the reduce adds the residual and normalises the updated rows in one pass
+                hipError_t e = launch_tile32<128, 128, EPI, true, 2>(st, A, B, C, work, M, N, K, ldc, split, splits,
+                                                                     kchunk);
+                if (e != hipSuccess)
+                    return e;
+                // 512 threads a row (one 16-byte vector each at width 4096) keep a row's partial loads in flight
+                gemm_resid_norm_kernel<<<M, 512, 0, st>>>(work, C, M, N, splits, norm->w, norm->y, norm->eps);
+                *normed = true;
+                return hipGetLastError();
+            }
         return launch_shape32<128, 128, EPI>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk, 0, rope);
     }
     if constexpr (EPI == GEMM_SWIGLU || EPI == GEMM_QKV_ROPE)
@@ -790,22 +843,35 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
 
 hipError_t launch_gemm(hipStream_t st, int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, uint32_t M,
                        uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, int cu_count, float *work,
-                       size_t work_elems, const GemmRope *rope)
+                       size_t work_elems, const GemmRope *rope, const GemmNorm *norm)
 {
     if (K % 8 != 0 || K < 8 || M == 0 || N == 0)
         return hipErrorInvalidValue;
     switch (epi)
     {
     case GEMM_PLAIN:
-        return launch_epi_gemm<GEMM_PLAIN>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count, nullptr);
+        return launch_epi_gemm<GEMM_PLAIN>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count, nullptr,
+                                             nullptr, nullptr);
     case GEMM_SILU_HI:
-        return launch_epi_gemm<GEMM_SILU_HI>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count, nullptr);
+        return launch_epi_gemm<GEMM_SILU_HI>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count, nullptr,
+                                             nullptr, nullptr);
     case GEMM_RESID:
-        return launch_epi_gemm<GEMM_RESID>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count, nullptr);
+    {
+        if (norm && (ldc != N || N % 8 != 0))
+            return hipErrorInvalidValue;
+        bool normed = false;
+        hipError_t e = launch_epi_gemm<GEMM_RESID>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count,
+                                                   nullptr, norm, &normed);
+        if (e != hipSuccess || !norm || normed)
+            return e;
+        return launch_rmsnorm_rows(st, C, norm->w, norm->y, M, N, norm->eps);
+    }
     case GEMM_SWIGLU:
-        return launch_epi_gemm<GEMM_SWIGLU>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count, nullptr);
+        return launch_epi_gemm<GEMM_SWIGLU>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count, nullptr,
+                                             nullptr, nullptr);
     case GEMM_QKV_ROPE:
-        return launch_epi_gemm<GEMM_QKV_ROPE>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count, rope);
+        return launch_epi_gemm<GEMM_QKV_ROPE>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count, rope,
+                                              nullptr, nullptr);
     default:
         return hipErrorInvalidValue;
     }

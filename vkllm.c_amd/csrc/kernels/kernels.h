@@ -189,12 +189,20 @@ struct GemmRope
     const float *cs;     // [M][hd / 2][2]: cos and sin of (offset + m) / base^(2w/hd), from launch_rope_table
     uint32_t offset, D, hd, ctx;
 };
+// GEMM_RESID followed by y[m] = RMSNorm(C[m]) * w (ldc == N; the norm of launch_rmsnorm_rows)
+struct GemmNorm
+{
+    const float *w;
+    uint16_t *y;
+    float eps;
+};
 // C[M, N] (row stride ldc) = A[M, K] . B[N, K]^T, fp16 operands, fp32 accumulation on MFMA. K % 8 == 0.
 // `work` (work_elems floats) holds split-K partial tiles for short prompts; with too little of it K is not split.
-// `rope` is read by GEMM_QKV_ROPE only.
+// `rope` is read by GEMM_QKV_ROPE only; `norm` (GEMM_RESID only) adds the RMSNorm of the updated rows, fused into
+// the split-K reduce when K is split.
 hipError_t launch_gemm(hipStream_t st, int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, uint32_t M,
                        uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, int cu_count, float *work,
-                       size_t work_elems, const GemmRope *rope = nullptr);
+                       size_t work_elems, const GemmRope *rope = nullptr, const GemmNorm *norm = nullptr);
 // cs[s][w] = (cos f, sin f) with f = (offset + s) / freqs[w], s < S, w < hd / 2 (the angles launch_rope_kv uses)
 hipError_t launch_rope_table(hipStream_t st, float *cs, const float *freqs, uint32_t offset, uint32_t S,
                              uint32_t hd);
