@@ -254,6 +254,11 @@ def main():
             except vk.VkllmError:
                 continue
             attn_long = True
+        elif name == "fused_attn_o" and not attn_o:
+            try:  # optional kernel: the device may not hold its two parts at once for this shape
+                avg_ns = model.time_kernel(name, reps)
+            except vk.VkllmError:
+                continue
         else:
             avg_ns = model.time_kernel(name, reps)
         if attn_long and name in ("fused_attn_scores", "fused_attn_pv"):

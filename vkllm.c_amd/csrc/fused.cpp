@@ -45,6 +45,7 @@ struct FusedState
     uint32_t *att_long_sync = nullptr; // per-head counters of the one-kernel long-cache attention, zero between launches
     float *gemm_work = nullptr;    // split-K partial tiles of short-prompt prefill GEMMs
     uint32_t att_cmax = 0, att_chunk = 0;
+    uint32_t attn_max_groups = 8; // dim slices per head of the short-cache attention, at most (VKLLM_ATTN_GROUPS)
     // decode attention in one kernel up to this many positions, in two kernels beyond (VKLLM_ATTN_SMALL_MAX)
     uint32_t attn_small_max = 0;
     // one-kernel attention and the output projection in one launch (VKLLM_ATTN_O=1; the default is two launches,
@@ -180,7 +181,9 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         shape.H = mp->H;
         shape.hd = mp->hd;
         shape.ctx = mp->ctx;
-        shape.groups = vk::attn_groups(mp->H, mp->hd, 8);
+        const char *ag = getenv("VKLLM_ATTN_GROUPS");
+        fs->attn_max_groups = ag && *ag ? (uint32_t)strtoul(ag, nullptr, 10) : 8u;
+        shape.groups = vk::attn_groups(mp->H, mp->hd, fs->attn_max_groups);
         const uint32_t limit = vk::attn_small_limit(shape);
         small = small < limit ? small : limit;
         fs->attn_small_max = small < mp->ctx ? small : mp->ctx;
@@ -295,7 +298,7 @@ static hipError_t launch_decode_kernel(vkllm_context *ctx, ModelPriv *mp, Kernel
         at.ctx = mp->ctx;
         at.cmax = fs->att_cmax;
         at.chunk = fs->att_chunk;
-        at.groups = vk::attn_groups(mp->H, hd, 8);
+        at.groups = vk::attn_groups(mp->H, hd, fs->attn_max_groups);
         at.scale = 1.0f / sqrtf((float)hd);
         at.long_sync = fs->att_long_sync;
         at.err = &fs->dio->err;
