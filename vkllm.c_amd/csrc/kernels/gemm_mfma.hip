@@ -8,12 +8,15 @@
 // bytes (the operand reads of 8 lanes then fall on distinct banks). A step is straight-line code whose instruction
 // stream group barriers lay out as MFMAs with, between them, the next 16-wide slice's operand reads, the next
 // step's global loads (first slice) and their stores into the other LDS buffer (last slice), so memory traffic
-// runs under the matrix pipe; one barrier per step.
+// runs under the matrix pipe; one barrier per step. Its epilogue stages the tile's fp16 outputs in the freed LDS and
+// stores 16-byte row chunks: plain, SiLU on columns >= split, residual add, the FFN's SwiGLU (reading [Wu; Wg] as
+// interleaved 32-row blocks), or the QKV product's RoPE with q and the K/V cache rows written directly.
 // gemm_kernel (other K): v_mfma_f32_16x16x32_f16, 128 x 128 or 128 x 64 tiles, the same double buffering, with the
-// K tail zeroed.
+// K tail zeroed (plain, SiLU and residual epilogues only).
 //
 // Narrow products split K over several workgroups; the fp32 partial tiles are added in split order by
-// gemm_splitk_reduce_kernel, which applies the epilogue. Tiles are ordered M-fastest and dealt to XCDs in
+// gemm_splitk_reduce_kernel, which applies the epilogue, or for a residual product followed by RMSNorm by
+// gemm_resid_norm_kernel, which also normalises the rows. Tiles are ordered M-fastest and dealt to XCDs in
 // contiguous runs so a run shares its B tiles in one L2. Global loads are unconditional at clamped addresses (a
 // guarded load compiles to a branch and a wait per load).
 #include <type_traits>
