@@ -241,12 +241,17 @@ __global__ __launch_bounds__(256) void attn_long_kernel(AttnDecodeArgs a)
     float *const st = a.stats + (size_t)h * a.cmax * 2;
     const uint16_t *Vh = a.vc + (size_t)h * a.ctx * a.hd;
 
-    // K and V rows of the chunk
+    // K rows of the chunk, then its scores; the V rows are requested only once the keys are in, so the keys of all
+    // chunks (which gate the statistics exchange) do not share the memory system with V, and V streams in while the
+    // statistics are exchanged
     const KeyLayout k = key_layout<256>(a.q + (size_t)h * a.hd, a.hd);
     const u32x4 *Kv = (const u32x4 *)(a.kc + ((size_t)h * a.ctx + j0) * a.hd);
     constexpr int U = 8, UV = 16; // keys and V rows per thread: 256 of each per round trip at head_dim 128
     u32x4 ka[U], kb[U];
     load_keys<U>(k, Kv, k.ks, n - 1, ka, kb);
+
+    // scores and the chunk's statistics (attn_scores_kernel)
+    score_keys<U>(k, ka, kb, k.ks, n, a.scale, sm);
     const uint32_t vpr = a.hd / 8, lpr = lanes_pow2(vpr), rpp = 256 / lpr;
     const uint32_t kl = tid % lpr, ks = tid / lpr;
     const u32x4 *Vv = (const u32x4 *)(Vh + (size_t)j0 * a.hd) + min(kl, vpr - 1);
@@ -254,9 +259,6 @@ __global__ __launch_bounds__(256) void attn_long_kernel(AttnDecodeArgs a)
 #pragma unroll
     for (int t = 0; t < UV; ++t)
         vv[t] = Vv[(size_t)min(ks + rpp * t, n - 1) * vpr];
-
-    // scores and the chunk's statistics (attn_scores_kernel)
-    score_keys<U>(k, ka, kb, k.ks, n, a.scale, sm);
     __syncthreads();
     float mx = -FLT_MAX;
     for (uint32_t j = tid; j < n; j += 256)
