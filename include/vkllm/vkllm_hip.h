@@ -87,7 +87,7 @@ extern vkllm_err_t vkllm_hip_token_loop(struct vkllm_context *context, struct vk
  * C[M, N] (row stride ldc >= N) = A[M, K] . B[N, K]^T with fp16 operands and fp32 accumulation (K % 8 == 0), then
  * the epilogue `epi`: 0 C = fp16(acc); 1 columns >= split fp16(silu(acc)), the others fp16(acc); 2 C =
  * fp16(C + fp16(acc)) (C holds the residual on entry); 3 (B = [Wu; Wg] with split = F rows each, N = 2F, N % 64 ==
- * 0, K % 64 == 0, ldc >= F) C[m][f] = fp16(fp16(A[m] . Wu[f]) * fp16(silu(A[m] . Wg[f]))), the FFN's SwiGLU, for
+ * 0, K % 64 == 0, ldc >= F, ldc % 8 == 0, C 16-byte aligned) C[m][f] = fp16(fp16(A[m] . Wu[f]) * fp16(silu(A[m] . Wg[f]))), the FFN's SwiGLU, for
  * f < F. `work` (work_elems floats, device memory, may be NULL with
  * work_elems 0) holds split-K partial tiles; with too little of it K is not split. This is the kernel behind the
  * fused step's matmul nodes (src/core/vkllm_op_matmul.c), exposed so that its tile and split choices can be checked

@@ -661,7 +661,8 @@ extern "C" vkllm_err_t vkllm_hip_gemm(struct vkllm_context *ctx, int epi, const 
 {
     _CHECK_ARGS(ctx && A && B && C && M > 0 && N > 0 && K >= 8 && K % 8 == 0);
     _CHECK_ARGS(epi == vk::GEMM_PLAIN || epi == vk::GEMM_SILU_HI || epi == vk::GEMM_RESID || epi == vk::GEMM_SWIGLU);
-    _CHECK_ARGS(epi == vk::GEMM_SWIGLU ? (K % 64 == 0 && N % 64 == 0 && split * 2 == N && ldc >= split) : ldc >= N);
+    _CHECK_ARGS(epi == vk::GEMM_SWIGLU ? (K % 64 == 0 && N % 64 == 0 && split * 2 == N && ldc >= split && ldc % 8 == 0)
+                                       : ldc >= N);
     _CHECK_ARGS(work != nullptr || work_elems == 0);
     hipStream_t st = ctx->device->stream;
     KTRY(ctx, KID_F_GEMM,

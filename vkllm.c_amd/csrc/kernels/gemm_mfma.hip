@@ -558,45 +558,58 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float *wo
                                                                  uint32_t splits, uint32_t n_base, GemmRope rope)
 {
     const uint64_t total = (uint64_t)M * N;
+    // 8 consecutive columns per step (N % 64 == 0 for these epilogues): 16-byte partial loads and output stores
+    auto sum8 = [&](size_t at, float *v) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            v[k] = 0.f;
+        for (uint32_t z = 0; z < splits; ++z)
+        {
+            const float4 *p = (const float4 *)(work + (size_t)z * total + at);
+            const float4 a = p[0], b = p[1];
+            v[0] += a.x;
+            v[1] += a.y;
+            v[2] += a.z;
+            v[3] += a.w;
+            v[4] += b.x;
+            v[5] += b.y;
+            v[6] += b.z;
+            v[7] += b.w;
+        }
+    };
     if constexpr (EPI == GEMM_QKV_ROPE)
     {
-        // one RoPE pair (columns 2p, 2p + 1) per step
-        const uint32_t half = N / 2;
-        const uint64_t pairs = (uint64_t)M * half;
-        for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < pairs; i += (uint64_t)gridDim.x * 256)
+        const uint32_t per_row = N / 8;
+        const uint64_t chunks = (uint64_t)M * per_row;
+        for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < chunks; i += (uint64_t)gridDim.x * 256)
         {
-            const uint32_t m = (uint32_t)(i / half), n = 2 * (uint32_t)(i % half);
-            const size_t at = (size_t)m * N + n;
-            float v0 = 0.f, v1 = 0.f;
-            for (uint32_t z = 0; z < splits; ++z)
-            {
-                v0 += work[(size_t)z * total + at];
-                v1 += work[(size_t)z * total + at + 1];
-            }
-            const uint32_t a = n_base + n, region = (a >= rope.D) + (a >= 2 * rope.D), c = a - region * rope.D;
-            const uint32_t head = c / rope.hd, dim = c % rope.hd;
-            const float q0 = h2f(f2h(v0)), q1 = h2f(f2h(v1));
-            rope_store(rope, m, region, c, head, dim, q0, q1);
-            rope_store(rope, m, region, c + 1, head, dim + 1, q1, q0);
+            const uint32_t m = (uint32_t)(i / per_row), n = 8 * (uint32_t)(i % per_row);
+            float v[8];
+            sum8((size_t)m * N + n, v);
+            u32x4 h;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                h[k] = pack2(f2h(v[2 * k]), f2h(v[2 * k + 1]));
+            rope_store8(rope, m, n_base + n, h);
         }
         return;
     }
     if constexpr (EPI == GEMM_SWIGLU)
     {
-        // one output per (row, up column); N % 64 == 0
-        const uint32_t half = N / 2;
-        const uint64_t outs = (uint64_t)M * half;
-        for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < outs; i += (uint64_t)gridDim.x * 256)
+        // 8 output columns f..f + 7 (inside one 32-column block): up columns c..c + 7, gate columns c + 32..c + 39
+        const uint32_t per_row = N / 16;
+        const uint64_t chunks = (uint64_t)M * per_row;
+        for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < chunks; i += (uint64_t)gridDim.x * 256)
         {
-            const uint32_t m = (uint32_t)(i / half), f = (uint32_t)(i % half), c = 64 * (f / 32) + f % 32;
-            const size_t at = (size_t)m * N + c;
-            float up = 0.f, gate = 0.f;
-            for (uint32_t z = 0; z < splits; ++z)
-            {
-                up += work[(size_t)z * total + at];
-                gate += work[(size_t)z * total + at + 32];
-            }
-            C[(size_t)m * ldc + swiglu_col(n_base + c)] = swiglu_out(up, gate);
+            const uint32_t m = (uint32_t)(i / per_row), f = 8 * (uint32_t)(i % per_row), c = 64 * (f / 32) + f % 32;
+            float up[8], gate[8];
+            sum8((size_t)m * N + c, up);
+            sum8((size_t)m * N + c + 32, gate);
+            u32x4 o;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                o[k] = pack2(swiglu_out(up[2 * k], gate[2 * k]), swiglu_out(up[2 * k + 1], gate[2 * k + 1]));
+            *(u32x4 *)(C + (size_t)m * ldc + swiglu_col(n_base + c)) = o;
         }
         return;
     }
@@ -756,7 +769,7 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
     if ((uint64_t)N * K >= (1ull << 32)) // B row offsets are 32-bit
         return hipErrorInvalidValue;
     if constexpr (EPI == GEMM_SWIGLU)
-        if (K % kBK != 0 || N % 64 != 0 || N != 2 * split)
+        if (K % kBK != 0 || N % 64 != 0 || N != 2 * split || ldc % 8 != 0 || (uintptr_t)C % 16 != 0)
             return hipErrorInvalidValue;
     if (K % kBK == 0)
     {
