@@ -84,12 +84,13 @@ extern vkllm_err_t vkllm_hip_token_loop(struct vkllm_context *context, struct vk
                                         uint32_t n_steps, uint32_t *ids, uint64_t *step_ns, uint64_t *phase_ns);
 
 /* The prompt-step GEMM on caller-owned device memory, on the context's stream; returns when C is written.
- * C[M, N] (row stride ldc >= N) = A[M, K] . B[N, K]^T with fp16 operands and fp32 accumulation (K % 8 == 0), then
- * the epilogue `epi`: 0 C = fp16(acc); 1 columns >= split fp16(silu(acc)), the others fp16(acc); 2 C =
- * fp16(C + fp16(acc)) (C holds the residual on entry); 3 (B = [Wu; Wg] with split = F rows each, N = 2F, N % 64 ==
- * 0, K % 64 == 0, ldc >= F, ldc % 8 == 0, C 16-byte aligned) C[m][f] = fp16(fp16(A[m] . Wu[f]) * fp16(silu(A[m] . Wg[f]))), the FFN's SwiGLU, for
- * f < F. `work` (work_elems floats, device memory, may be NULL with
- * work_elems 0) holds split-K partial tiles; with too little of it K is not split. This is the kernel behind the
+ * C[M, N] (row stride ldc >= N) = A[M, K] . B[N, K]^T with fp16 operands and fp32 accumulation (K % 8 == 0; A, B
+ * and work 16-byte aligned), then the epilogue `epi`: 0 C = fp16(acc); 1 columns >= split fp16(silu(acc)), the
+ * others fp16(acc); 2 C = fp16(C + fp16(acc)) (C holds the residual on entry); 3 (B = [Wu; Wg] with split = F rows
+ * each, N = 2F, N % 64 == 0, K % 64 == 0, ldc >= F, ldc % 8 == 0, C 16-byte aligned) C[m][f] =
+ * fp16(fp16(A[m] . Wu[f]) * fp16(silu(A[m] . Wg[f]))), the FFN's SwiGLU, for f < F. `work` (work_elems floats,
+ * device memory, may be NULL with work_elems 0) holds split-K partial tiles; with too little of it K is not split.
+ * Arguments outside these rules return VKLLM_ERR_ARGS. This is the kernel behind the
  * fused step's matmul nodes (src/core/vkllm_op_matmul.c), exposed so that its tile and split choices can be checked
  * and timed at any shape. */
 extern vkllm_err_t vkllm_hip_gemm(struct vkllm_context *context, int epi, const uint16_t *A, const uint16_t *B,

@@ -134,3 +134,8 @@ def test_gemm_rejects_bad_arguments(ctx, vk):
     assert L.vkllm_hip_gemm(ctx.vp, SWIGLU, p, p, p, 4, 128, 96, 64, 64, None, 0) == vk.ERR_ARGS  # K % 64 != 0
     assert L.vkllm_hip_gemm(ctx.vp, SWIGLU, p, p, p, 4, 96, 64, 48, 48, None, 0) == vk.ERR_ARGS  # N % 64 != 0
     assert L.vkllm_hip_gemm(ctx.vp, PLAIN, p, p, p, 4, 4, 16, 4, 0, None, 64) == vk.ERR_ARGS  # work size, no work
+    q = ctypes.c_void_p(18)  # 2-byte aligned only
+    assert L.vkllm_hip_gemm(ctx.vp, PLAIN, q, p, p, 4, 4, 16, 4, 0, None, 0) == vk.ERR_ARGS  # A not 16-byte aligned
+    assert L.vkllm_hip_gemm(ctx.vp, PLAIN, p, q, p, 4, 4, 16, 4, 0, None, 0) == vk.ERR_ARGS  # B not 16-byte aligned
+    assert L.vkllm_hip_gemm(ctx.vp, PLAIN, p, p, p, 4, 4, 16, 4, 0, q, 64) == vk.ERR_ARGS  # work not aligned
+    assert L.vkllm_hip_gemm(ctx.vp, SWIGLU, p, p, q, 4, 128, 64, 64, 64, None, 0) == vk.ERR_ARGS  # C not aligned

@@ -664,6 +664,9 @@ extern "C" vkllm_err_t vkllm_hip_gemm(struct vkllm_context *ctx, int epi, const 
     _CHECK_ARGS(epi == vk::GEMM_SWIGLU ? (K % 64 == 0 && N % 64 == 0 && split * 2 == N && ldc >= split && ldc % 8 == 0)
                                        : ldc >= N);
     _CHECK_ARGS(work != nullptr || work_elems == 0);
+    // the tiles read A, B and the split-K partials as 16-byte vectors; the SwiGLU reduce stores C as 16-byte vectors
+    _CHECK_ARGS(((uintptr_t)A | (uintptr_t)B | (uintptr_t)work) % 16 == 0);
+    _CHECK_ARGS(epi != vk::GEMM_SWIGLU || (uintptr_t)C % 16 == 0);
     hipStream_t st = ctx->device->stream;
     KTRY(ctx, KID_F_GEMM,
          vk::launch_gemm(st, epi, A, B, C, M, N, K, ldc, split, ctx->device->cu_count, work, (size_t)work_elems));
