@@ -669,7 +669,7 @@ uint32_t attn_groups(uint32_t H, uint32_t hd, uint32_t max_groups)
 {
     // the largest divisor of the row's 16-byte vectors that is <= max_groups while H * G stays <= 1024 blocks
     uint32_t best = 1;
-    for (uint32_t g = 1; g <= max_groups; ++g)
+    for (uint32_t g = 1; g <= max_groups && g <= hd / 8; ++g)
         if ((hd / 8) % g == 0 && H * g <= 1024)
             best = g;
     return best;
