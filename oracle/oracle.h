@@ -70,11 +70,11 @@ int oracle_is_transposed_b(const oracle_tensor *a, const oracle_tensor *b, const
 
 /* VKLLM_OP_MATMUL: out = act(scale * A . B) with B [N,K] when oracle_is_transposed_b(), else [K,N].
  * Batch dims of size 1 broadcast. act 1 = SiLU v/(1+exp(-v)).
- * src/core/vkllm_op_matmul.c:32-63,317-329, src/shaders/vkllm_mat_mul_vec.comp:115-171,
+ * src/core/vkllm_op_matmul.c:32-63,317-329, src/shaders/vkllm_mat_mul_vec.comp:94-150,
  * src/shaders/vkllm_matmul_t1.comp:90-251, src/shaders/vkllm_matmul_t0.comp:92-245 */
 int oracle_matmul(const oracle_tensor *a, const oracle_tensor *b, oracle_tensor *out, float scale, int32_t act);
 
-/* VKLLM_OP_EMBEDDING: src/core/vkllm_op_embedding.c:40-55, src/shaders/vkllm_embedding.comp:138-167 */
+/* VKLLM_OP_EMBEDDING: src/core/vkllm_op_embedding.c:40-55, src/shaders/vkllm_embedding.comp:41-70 */
 int oracle_embedding(const oracle_tensor *idx, const oracle_tensor *table, oracle_tensor *out, uint32_t unk_tok);
 
 /* VKLLM_OP_RMSNORM: y = (x*w) * 1/sqrt(sum(x^2)/W + eps); src/shaders/vkllm_rmsnorm.comp:31-82 */

@@ -14,6 +14,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <unistd.h>
 
 /* GGUF v3 constants (public GGUF specification; the reference reads them through antirez/gguf-tools) */
 enum
@@ -267,6 +268,58 @@ static void gen_weights(const oracle_llama_cfg *cfg, uint64_t seed, uint32_t id,
     if (nt > 1)
         for (int t = 0; t < nt; ++t)
             pthread_join(th[t], NULL);
+}
+
+/* ---- parallel loops of the forward step ----
+ * fn(arg, i) for i in [0, n), split into contiguous ranges over up to ORACLE_THREADS threads (default: the online
+ * CPUs, at most 16) when the loop does enough work. Every index is computed by exactly one thread with the same arithmetic in the same order, so
+ * the results do not depend on the thread count. */
+typedef void (*par_fn)(void *arg, size_t i);
+typedef struct
+{
+    par_fn fn;
+    void *arg;
+    size_t begin, end;
+} par_job;
+
+static void *par_worker(void *p)
+{
+    par_job *j = (par_job *)p;
+    for (size_t i = j->begin; i < j->end; ++i)
+        j->fn(j->arg, i);
+    return NULL;
+}
+
+static int par_threads(void)
+{
+    const char *e = getenv("ORACLE_THREADS");
+    long n = e && *e ? strtol(e, NULL, 10) : sysconf(_SC_NPROCESSORS_ONLN);
+    return n < 1 ? 1 : (n > 16 ? 16 : (int)n);
+}
+
+static void par_for(size_t n, par_fn fn, void *arg, double work)
+{
+    /* thread start-up costs ~20 us: small loops (under ~4M multiply-adds) stay on the calling thread */
+    int nt = work < 4e6 ? 1 : par_threads();
+    if ((size_t)nt > n)
+        nt = (int)n;
+    if (nt <= 1)
+    {
+        for (size_t i = 0; i < n; ++i)
+            fn(arg, i);
+        return;
+    }
+    pthread_t th[16];
+    par_job jobs[16];
+    size_t chunk = (n + nt - 1) / nt;
+    for (int t = 0; t < nt; ++t)
+    {
+        size_t b = chunk * t, e = b + chunk < n ? b + chunk : n;
+        jobs[t] = (par_job){fn, arg, b < e ? b : e, e};
+        pthread_create(&th[t], NULL, par_worker, &jobs[t]);
+    }
+    for (int t = 0; t < nt; ++t)
+        pthread_join(th[t], NULL);
 }
 
 int oracle_gguf_write_random(const char *path, const oracle_llama_cfg *c, uint64_t seed)
@@ -697,27 +750,41 @@ const uint16_t *oracle_model_weight(const oracle_model *m, uint32_t id, size_t *
 /* forward step */
 
 /* y[s][n] = fp16(act(scale * sum_k x[s][k] W[n][k])): VKLLM_OP_MATMUL with a [N,K] weight
- * (src/shaders/vkllm_mat_mul_vec.comp:132-170 for S == 1, src/shaders/vkllm_matmul_t1.comp:156-250 otherwise) */
+ * (src/shaders/vkllm_mat_mul_vec.comp:94-150 for S == 1, src/shaders/vkllm_matmul_t1.comp:156-250 otherwise) */
+typedef struct
+{
+    const double *xd;
+    const uint16_t *W;
+    uint16_t *y;
+    uint32_t S, K, N;
+    int act;
+} linear_job;
+
+static void linear_row(void *p, size_t n)
+{
+    const linear_job *j = (const linear_job *)p;
+    const uint32_t K = j->K;
+    const uint16_t *w = j->W + n * K;
+    for (uint32_t s = 0; s < j->S; ++s)
+    {
+        const double *xs = j->xd + (size_t)s * K;
+        double acc = 0.0;
+        for (uint32_t k = 0; k < K; ++k)
+            acc += xs[k] * (double)h2f(w[k]);
+        float v = (float)acc * 1.0f;
+        if (j->act)
+            v = v / (1.0f + expf(-v));
+        j->y[(size_t)s * j->N + n] = oracle_f32_to_f16(v);
+    }
+}
+
 static void linear(const uint16_t *x, const uint16_t *W, uint16_t *y, uint32_t S, uint32_t K, uint32_t N, int act)
 {
     double *xd = (double *)malloc(sizeof(double) * K * S);
     for (size_t i = 0; i < (size_t)K * S; ++i)
         xd[i] = h2f(x[i]);
-    for (uint32_t n = 0; n < N; ++n)
-    {
-        const uint16_t *w = W + (size_t)n * K;
-        for (uint32_t s = 0; s < S; ++s)
-        {
-            const double *xs = xd + (size_t)s * K;
-            double acc = 0.0;
-            for (uint32_t k = 0; k < K; ++k)
-                acc += xs[k] * (double)h2f(w[k]);
-            float v = (float)acc * 1.0f;
-            if (act)
-                v = v / (1.0f + expf(-v));
-            y[(size_t)s * N + n] = oracle_f32_to_f16(v);
-        }
-    }
+    linear_job j = {xd, W, y, S, K, N, act};
+    par_for(N, linear_row, &j, (double)N * S * K);
     free(xd);
 }
 
@@ -746,6 +813,66 @@ static void add_rows(uint16_t *h, const uint16_t *o, size_t n)
         h[i] = oracle_f32_to_f16(h2f(h[i]) + h2f(o[i]));
 }
 
+/* One attention row: head hh, query row s of the step (src/models/vkllm_llama2_layers.c:223-281). */
+typedef struct
+{
+    const uint16_t *rq; /* [H][S][hd] rotated queries */
+    const uint16_t *kc, *vc; /* the layer's caches [H][ctx][hd] */
+    uint16_t *att; /* [S][D] */
+    uint32_t S, offset, kv, D, hd, ctx;
+    float scale;
+} attn_job;
+
+static void attn_row(void *p, size_t i)
+{
+    const attn_job *a = (const attn_job *)p;
+    const uint32_t S = a->S, offset = a->offset, kv = a->kv, D = a->D, hd = a->hd, ctx = a->ctx;
+    const uint32_t hh = (uint32_t)(i / S), s = (uint32_t)(i % S);
+    const uint16_t *kc = a->kc, *vc = a->vc;
+    uint16_t *att = a->att;
+    const float scale = a->scale;
+    uint16_t *sc = (uint16_t *)malloc((size_t)kv * 2);
+    uint16_t *pr = (uint16_t *)malloc((size_t)kv * 2);
+    const uint16_t *qr = a->rq + ((size_t)hh * S + s) * hd;
+
+    /* scores = fp16(scale * q.k) (src/models/vkllm_llama2_layers.c:223-233) */
+    for (uint32_t j = 0; j < kv; ++j)
+    {
+        const uint16_t *kr = kc + ((size_t)hh * ctx + j) * hd;
+        double acc = 0.0;
+        for (uint32_t d = 0; d < hd; ++d)
+            acc += (double)h2f(qr[d]) * (double)h2f(kr[d]);
+        sc[j] = oracle_f32_to_f16((float)acc * scale);
+    }
+    /* SOFTMAX seq_mask=1, offsets=offset (layers.c:237-245, softmax.comp:53-95) */
+    float mx = h2f(sc[0]);
+    for (uint32_t j = 0; j < kv; ++j)
+        mx = h2f(sc[j]) > mx ? h2f(sc[j]) : mx;
+    double sum = 0.0;
+    for (uint32_t j = 0; j <= s + offset && j < kv; ++j)
+        sum += expf(h2f(sc[j]) - mx);
+    float sf = (float)sum;
+    for (uint32_t j = 0; j < kv; ++j)
+        pr[j] = j > s + offset ? 0 : oracle_f32_to_f16(expf(h2f(sc[j]) - mx) / sf);
+    /* attn . V (layers.c:247-257). When kv == hd, is_transposed_b (src/core/vkllm_op_matmul.c:14-24)
+     * reads the [kv, hd] V slice as [N, K] and the product becomes attn . V^T. */
+    int transposed = (kv == hd);
+    for (uint32_t n = 0; n < hd; ++n)
+    {
+        double acc = 0.0;
+        for (uint32_t j = 0; j < kv; ++j)
+        {
+            uint16_t vv = transposed ? vc[((size_t)hh * ctx + n) * hd + j] : vc[((size_t)hh * ctx + j) * hd + n];
+            acc += (double)h2f(pr[j]) * (double)h2f(vv);
+        }
+        /* permute + COPY into [S, H*hd] (layers.c:259-281) */
+        att[(size_t)s * D + (size_t)hh * hd + n] = oracle_f32_to_f16((float)acc * 1.0f);
+    }
+
+    free(sc);
+    free(pr);
+}
+
 int oracle_model_step(oracle_model *m, const uint32_t *toks, uint32_t S, uint32_t offset, uint32_t *out_ids,
                       uint16_t *logits_out, uint16_t *hidden_out)
 {
@@ -766,8 +893,6 @@ int oracle_model_step(oracle_model *m, const uint32_t *toks, uint32_t S, uint32_
     uint16_t *o = (uint16_t *)malloc((size_t)S * D * 2);
     uint16_t *up = (uint16_t *)malloc((size_t)S * F * 2);
     uint16_t *gate = (uint16_t *)malloc((size_t)S * F * 2);
-    uint16_t *sc = (uint16_t *)malloc((size_t)kv * 2);
-    uint16_t *pr = (uint16_t *)malloc((size_t)kv * 2);
     uint16_t *logits = (uint16_t *)malloc((size_t)S * V * 2);
 
     /* EMBEDDING with unk = padding_token_id (src/models/vkllm_models_llama2.c:505-513) */
@@ -790,7 +915,7 @@ int oracle_model_step(oracle_model *m, const uint32_t *toks, uint32_t S, uint32_
         linear(xn, (const uint16_t *)m->tensors[tid_blk(l, K_Q)], q, S, D, D, 0);
         linear(xn, (const uint16_t *)m->tensors[tid_blk(l, K_K)], k, S, D, D, 0);
         linear(xn, (const uint16_t *)m->tensors[tid_blk(l, K_V)], v, S, D, D, 0);
-        /* views [S,D] -> [S,H,hd] -> [H,S,hd]; RoPE (normal style) at position offset + s (rope.comp:146-174);
+        /* views [S,D] -> [S,H,hd] -> [H,S,hd]; RoPE (normal style) at position offset + s (rope.comp:39-79);
          * KV append (update_rows) at row offset + s */
         for (uint32_t hh = 0; hh < H; ++hh)
             for (uint32_t s = 0; s < S; ++s)
@@ -810,44 +935,8 @@ int oracle_model_step(oracle_model *m, const uint32_t *toks, uint32_t S, uint32_
                     vc[dk] = v[src];
                     vc[dk + 1] = v[src + 1];
                 }
-        for (uint32_t hh = 0; hh < H; ++hh)
-            for (uint32_t s = 0; s < S; ++s)
-            {
-                const uint16_t *qr = rq + ((size_t)hh * S + s) * hd;
-                /* scores = fp16(scale * q.k) (src/models/vkllm_llama2_layers.c:223-233) */
-                for (uint32_t j = 0; j < kv; ++j)
-                {
-                    const uint16_t *kr = kc + ((size_t)hh * ctx + j) * hd;
-                    double acc = 0.0;
-                    for (uint32_t d = 0; d < hd; ++d)
-                        acc += (double)h2f(qr[d]) * (double)h2f(kr[d]);
-                    sc[j] = oracle_f32_to_f16((float)acc * scale);
-                }
-                /* SOFTMAX seq_mask=1, offsets=offset (layers.c:237-245, softmax.comp:53-95) */
-                float mx = h2f(sc[0]);
-                for (uint32_t j = 0; j < kv; ++j)
-                    mx = h2f(sc[j]) > mx ? h2f(sc[j]) : mx;
-                double sum = 0.0;
-                for (uint32_t j = 0; j <= s + offset && j < kv; ++j)
-                    sum += expf(h2f(sc[j]) - mx);
-                float sf = (float)sum;
-                for (uint32_t j = 0; j < kv; ++j)
-                    pr[j] = j > s + offset ? 0 : oracle_f32_to_f16(expf(h2f(sc[j]) - mx) / sf);
-                /* attn . V (layers.c:247-257). When kv == hd, is_transposed_b (src/core/vkllm_op_matmul.c:14-24)
-                 * reads the [kv, hd] V slice as [N, K] and the product becomes attn . V^T. */
-                int transposed = (kv == hd);
-                for (uint32_t n = 0; n < hd; ++n)
-                {
-                    double acc = 0.0;
-                    for (uint32_t j = 0; j < kv; ++j)
-                    {
-                        uint16_t vv = transposed ? vc[((size_t)hh * ctx + n) * hd + j] : vc[((size_t)hh * ctx + j) * hd + n];
-                        acc += (double)h2f(pr[j]) * (double)h2f(vv);
-                    }
-                    /* permute + COPY into [S, H*hd] (layers.c:259-281) */
-                    att[(size_t)s * D + (size_t)hh * hd + n] = oracle_f32_to_f16((float)acc * 1.0f);
-                }
-            }
+        attn_job aj = {rq, kc, vc, att, S, offset, kv, D, hd, ctx, scale};
+        par_for((size_t)H * S, attn_row, &aj, 2.0 * H * S * kv * hd);
         linear(att, (const uint16_t *)m->tensors[tid_blk(l, K_O)], o, S, D, D, 0);
         add_rows(h, o, (size_t)S * D);
 
@@ -883,8 +972,6 @@ int oracle_model_step(oracle_model *m, const uint32_t *toks, uint32_t S, uint32_
     free(o);
     free(up);
     free(gate);
-    free(sc);
-    free(pr);
     free(logits);
     return 0;
 }

@@ -188,7 +188,7 @@ int oracle_is_transposed_b(const oracle_tensor *a, const oracle_tensor *b, const
 
 /* The broadcast rule of src/core/vkllm_op_matmul.c:37-63 (boardcast_type) reads an operand's batch/channel
  * stride only where that operand's dimension is not 1, which for operands whose dims are 1 or equal to the
- * output's is numpy broadcasting. The GEMV path (src/shaders/vkllm_mat_mul_vec.comp:127-165) honours all strides;
+ * output's is numpy broadcasting. The GEMV path (src/shaders/vkllm_mat_mul_vec.comp:113-141) honours all strides;
  * the GEMM path (src/shaders/vkllm_matmul_t1.comp:161,178,242) assumes unit stride along W. The oracle honours
  * all strides. */
 int oracle_matmul(const oracle_tensor *a, const oracle_tensor *b, oracle_tensor *out, float scale, int32_t act)
@@ -230,7 +230,7 @@ int oracle_matmul(const oracle_tensor *a, const oracle_tensor *b, oracle_tensor 
     return 0;
 }
 
-/* src/core/vkllm_op_embedding.c:40-55 (checks) and src/shaders/vkllm_embedding.comp:138-167: one output row per
+/* src/core/vkllm_op_embedding.c:40-55 (checks) and src/shaders/vkllm_embedding.comp:41-70: one output row per
  * index; an index >= the table's row count reads row `unk_tok`. The output row offset is
  * c*out.strides[0] + h*out.strides[1] + w*out.strides[2] (the shader's index shift, which for the [1,1,1,S]
  * index tensor of the model is row w). */

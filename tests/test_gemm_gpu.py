@@ -46,6 +46,12 @@ CASES = [
     (128, 22016, 1216, SWIGLU, 11008, True),  # 128 tokens: whole K per 128 x 128 tile, four steps in flight
     (128, 12288, 1024, SWIGLU, 6144, True),   # 128 x 128 tiles with split K and the reduce
     (100, 3072, 512, SWIGLU, 1536, False),    # ragged M, no work buffer
+    # the LLaMA-2-13B prompt products at 2048 tokens with their real K (dim 5120, FFN 13824)
+    (2048, 15360, 5120, PLAIN, 0, True),      # [Wq; Wk; Wv]
+    (2048, 5120, 5120, RESID, 0, True),       # Wo + residual: 160 tiles of 256 x 256
+    (2048, 27648, 5120, SWIGLU, 13824, True),  # [Wu; Wg] with SwiGLU: three full rounds and the split-K tail
+    (2048, 5120, 13824, RESID, 0, True),      # Wd + residual
+    (2048, 32000, 5120, PLAIN, 0, True),      # logits
     (77, 1000, 256, PLAIN, 0, True),          # ragged, one partial tile row
     (77, 1000, 1000, PLAIN, 0, True),         # K % 64 != 0: 128 x 64 tiles
     (300, 1000, 1000, SILU_HI, 500, True),    # K % 64 != 0, M > 128

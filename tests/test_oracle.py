@@ -434,3 +434,74 @@ def test_oracle_token_loop_tiny_deterministic(oracle, tiny_gguf):
     m2 = oracle.Model(tiny_gguf)
     b, _ = m2.token_loop(p, 8)
     assert a.tolist() == b.tolist()
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# the token loop (tests/vkllm_test_infer_gguf.c:181-272): step 0 runs the whole prompt at offset 0, every later step
+# the previous step's output id at offset += S (:255-269); the id fed back is the LAST row's (extract_output_tok,
+# :100-120)
+def chained_steps(m, prompt, n_steps):
+    """The driver's protocol written out with explicit oracle_model_step calls."""
+    toks, offset, ids, logits = np.asarray(prompt, np.uint32), 0, [], []
+    for _ in range(n_steps):
+        out, lg, _ = m.step(toks, offset, want_logits=True)
+        ids.append(int(out[len(toks) - 1]))
+        logits.append(lg[len(toks) - 1])
+        offset += len(toks)
+        toks = np.array([ids[-1]], np.uint32)
+    return np.array(ids, np.uint32), np.stack(logits)
+
+
+@pytest.mark.parametrize("prompt_len", [1, 7])
+def test_oracle_token_loop_equals_chained_steps(oracle, prompt_len):
+    cfg = oracle.make_cfg(n_layer=2, dim=64, n_head=4, ffn=96, vocab=300, ctx=64)
+    prompt = oracle.prompt_tokens(21, prompt_len, cfg.vocab)
+    a = oracle.Model(cfg=cfg, seed=12)
+    ids, logits = a.token_loop(prompt, 12, want_logits=True)
+    b = oracle.Model(cfg=cfg, seed=12)
+    want_ids, want_logits = chained_steps(b, prompt, 12)
+    assert ids.tolist() == want_ids.tolist()
+    assert np.array_equal(logits.view(np.uint16), want_logits.view(np.uint16))
+
+
+def test_oracle_token_loop_vs_float64_recompute(oracle):
+    """Teacher-forced against a float64 LLaMA-2 that recomputes the whole sequence (prompt + ids so far) at every
+    step, with no KV cache: the loop's logits for step t must be the float64 model's last-row logits for that
+    sequence (within 2e-2), and each id its arg max (or, at a float64 top-2 gap under 2e-2, one of the two). A loop
+    that fed back another row's id, advanced the offset wrongly or re-used a stale cache row fails this.
+    Two heads of 32 keep kv below head_dim: at kv == head_dim the reference's shape rule transposes attn . V for
+    that one step (src/core/vkllm_op_matmul.c:14-24), which a whole-sequence recompute cannot reproduce."""
+    cfg = oracle.make_cfg(n_layer=2, dim=64, n_head=2, ffn=96, vocab=300, ctx=64)
+    m = oracle.Model(cfg=cfg, seed=13)
+    prompt = oracle.prompt_tokens(22, 9, cfg.vocab)
+    n = 10
+    ids, logits = m.token_loop(prompt, n, want_logits=True)
+    seq = list(map(int, prompt))
+    for t in range(n):
+        want = np_llama(m.weight, cfg, np.array(seq, np.int64))[-1]
+        err = np.max(np.abs(logits[t].astype(np.float64) - want))
+        assert err < 2e-2, f"step {t}: logits differ from the float64 recompute by {err}"
+        top = np.sort(want)[::-1]
+        if top[0] - top[1] >= 2e-2:
+            assert int(ids[t]) == int(np.argmax(want)), f"step {t}: id {ids[t]} != {np.argmax(want)}"
+        else:
+            assert int(ids[t]) in np.argsort(want)[::-1][:2].tolist()
+        seq.append(int(ids[t]))
+
+
+def test_oracle_token_loop_planted_offset_error_is_caught(oracle):
+    """The float64 recompute detects a loop that advances the offset by one position too many: the same chain with
+    offset += S + 1 gives logits far from the float64 model's (the check above is not blind to the offset)."""
+    cfg = oracle.make_cfg(n_layer=2, dim=64, n_head=2, ffn=96, vocab=300, ctx=64)
+    m = oracle.Model(cfg=cfg, seed=13)
+    prompt = oracle.prompt_tokens(22, 9, cfg.vocab)
+    toks, offset, seq, worst = prompt, 0, list(map(int, prompt)), 0.0
+    for _ in range(6):
+        out, lg, _ = m.step(toks, offset, want_logits=True)
+        if offset:
+            want = np_llama(m.weight, cfg, np.array(seq, np.int64))[-1]
+            worst = max(worst, float(np.max(np.abs(lg[-1].astype(np.float64) - want))))
+        offset += len(toks) + 1  # the planted mistake
+        seq.append(int(out[-1]))
+        toks = np.array([seq[-1]], np.uint32)
+    assert worst > 2e-2  # the recompute check's tolerance

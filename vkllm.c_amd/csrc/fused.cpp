@@ -59,6 +59,8 @@ struct FusedState
     bool rope_epi = true;
     // prompt steps: the RMSNorm after each residual product in its split-K reduce (VKLLM_NORM_EPI=0: a separate pass)
     bool norm_epi = true;
+    // polls of the bounded waits before they give up (VKLLM_SPIN_LIMIT; 0 forces the give-up path)
+    uint32_t long_spin_limit = vk::kAttnLongSpinLimit, attn_o_spin_limit = vk::kAttnOSpinLimit;
     // captured single-token steps: [0] with the one-kernel attention, [1] with the two-kernel attention
     hipGraph_t graph[2] = {nullptr, nullptr};
     hipGraphExec_t exec[2] = {nullptr, nullptr};
@@ -195,6 +197,9 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         fs->rope_epi = !(re && *re == '0');
         const char *ne = getenv("VKLLM_NORM_EPI");
         fs->norm_epi = !(ne && *ne == '0');
+        const char *sl = getenv("VKLLM_SPIN_LIMIT");
+        if (sl && *sl)
+            fs->long_spin_limit = fs->attn_o_spin_limit = (uint32_t)strtoul(sl, nullptr, 10);
         HIP_TRY(hipMalloc(&fs->att_scores, H * mp->ctx * sizeof(float)));
         HIP_TRY(hipMalloc(&fs->att_stats, H * C * 2 * sizeof(float)));
         HIP_TRY(hipMalloc(&fs->att_part, H * C * mp->hd * sizeof(float)));
@@ -302,6 +307,7 @@ static hipError_t launch_decode_kernel(vkllm_context *ctx, ModelPriv *mp, Kernel
         at.scale = 1.0f / sqrtf((float)hd);
         at.long_sync = fs->att_long_sync;
         at.err = &fs->dio->err;
+        at.spin_limit = kid == KID_F_ATTN_O ? fs->attn_o_spin_limit : fs->long_spin_limit;
         if (kid == KID_F_ATTN_LONG)
             return vk::launch_attn_long(st, at, cu);
         if (kid == KID_F_ATTN_SMALL)
@@ -480,6 +486,36 @@ vkllm_err_t fused_plan_init(vkllm_context *ctx, vkllm_graph *graph)
     return ensure_state(ctx, mp, p->S);
 }
 
+// Enqueues one single-token step: a replay of the captured graph for this attention variant (captured on first
+// use), or direct launches when graph replay or timing says so.
+static vkllm_err_t launch_decode_step(vkllm_context *ctx, ModelPriv *mp, bool small)
+{
+    FusedState *fs = mp->fs;
+    hipStream_t st = ctx->device->stream;
+    if (!ctx->device->graph_replay || ctx->device->timing)
+        return enqueue_decode(ctx, mp, small);
+    const int v = small ? 0 : 1;
+    if (!fs->exec[v])
+    {
+        HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
+        vkllm_err_t rc = enqueue_decode(ctx, mp, small);
+        hipGraph_t g = nullptr;
+        hipError_t ce = hipStreamEndCapture(st, &g);
+        if (rc != VKLLM_ERR_OK)
+        {
+            if (g)
+                (void)hipGraphDestroy(g);
+            return rc;
+        }
+        HIP_TRY(ce);
+        fs->graph[v] = g;
+        HIP_TRY(hipGraphInstantiate(&fs->exec[v], g, nullptr, nullptr, 0));
+    }
+    HIP_TRY(hipGraphLaunch(fs->exec[v], st));
+    fs->last_exec = v;
+    return VKLLM_ERR_OK;
+}
+
 vkllm_err_t fused_plan_run(vkllm_context *ctx, vkllm_graph *graph)
 {
     auto *p = (FusedPlan *)graph->plan;
@@ -500,42 +536,31 @@ vkllm_err_t fused_plan_run(vkllm_context *ctx, vkllm_graph *graph)
         fs->dio->err = 0;
         const uint64_t t0 = fs->trace ? host_ns() : 0;
         const bool small = p->offset + 1 <= fs->attn_small_max;
-        if (ctx->device->graph_replay && !ctx->device->timing)
-        {
-            const int v = small ? 0 : 1;
-            if (!fs->exec[v])
-            {
-                HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
-                vkllm_err_t rc = enqueue_decode(ctx, mp, small);
-                hipGraph_t g = nullptr;
-                hipError_t ce = hipStreamEndCapture(st, &g);
-                if (rc != VKLLM_ERR_OK)
-                {
-                    if (g)
-                        (void)hipGraphDestroy(g);
-                    return rc;
-                }
-                HIP_TRY(ce);
-                fs->graph[v] = g;
-                HIP_TRY(hipGraphInstantiate(&fs->exec[v], g, nullptr, nullptr, 0));
-            }
-            HIP_TRY(hipGraphLaunch(fs->exec[v], st));
-            fs->last_exec = v;
-        }
-        else
-            _CHECK(enqueue_decode(ctx, mp, small));
+        _CHECK(launch_decode_step(ctx, mp, small));
         const uint64_t t1 = fs->trace ? host_ns() : 0;
         HIP_TRY(hipStreamSynchronize(st));
-        fs->io_h[0] = ((volatile vk::DecodeIo *)fs->dio)->id;
         if (((volatile vk::DecodeIo *)fs->dio)->err)
         {
-            log_error("decode step at position %u: a kernel's wait for other workgroups gave up", p->offset);
-            // the launch that gave up may have left counters set: clear them for the next step
-            (void)hipMemset(fs->attn_sync, 0, vk::kAttnSyncWords * sizeof(uint32_t));
-            (void)hipMemset(fs->att_long_sync, 0, (size_t)mp->H * vk::kAttnLongStride * sizeof(uint32_t));
-            (void)hipDeviceSynchronize();
-            return VKLLM_ERR_VULKAN;
+            // A bounded wait between workgroups gave up (the GPU is shared or busy, so not every block of the launch
+            // was resident). Clear the counters that launch left, switch to the attention kernels that never wait,
+            // and run the step again: it starts from the embedding and rewrites the same cache rows, so a second run
+            // gives the step's result.
+            log_error("decode step at position %u: a kernel's wait for other workgroups gave up; running it again "
+                      "with attention kernels that do not wait",
+                      p->offset);
+            HIP_TRY(hipMemsetAsync(fs->attn_sync, 0, vk::kAttnSyncWords * sizeof(uint32_t), st));
+            HIP_TRY(hipMemsetAsync(fs->att_long_sync, 0, (size_t)mp->H * vk::kAttnLongStride * sizeof(uint32_t), st));
+            HIP_TRY(hipMemsetAsync(fs->att_count, 0, (size_t)mp->H * sizeof(uint32_t), st));
+            drop_graphs(fs);
+            fs->attn_long = false;
+            fs->attn_o = false;
+            fs->dio->err = 0;
+            _CHECK(launch_decode_step(ctx, mp, small));
+            HIP_TRY(hipStreamSynchronize(st));
+            if (((volatile vk::DecodeIo *)fs->dio)->err)
+                return VKLLM_ERR_VULKAN;
         }
+        fs->io_h[0] = ((volatile vk::DecodeIo *)fs->dio)->id;
         if (fs->trace)
         {
             fs->trace_steps += 1;

@@ -217,29 +217,57 @@ bool File::open(const char *path, std::string *err)
         *err = "truncated or malformed header";
         return false;
     }
-    size_t data_start = (size_t)(c.p - base);
-    data_start = (data_start + alignment - 1) / alignment * alignment;
+    // Every size below is checked by subtraction against what remains of the file, so no sum or product wraps.
+    const uint64_t header_end = (uint64_t)(c.p - base);
+    if (alignment > size)
+    {
+        *err = "alignment larger than the file";
+        return false;
+    }
+    const uint64_t data_start = (header_end + alignment - 1) / alignment * alignment;
+    if (data_start > size && !tensors.empty())
+    {
+        *err = "data section starts past end of file";
+        return false;
+    }
+    const uint64_t data_size = tensors.empty() ? 0 : size - data_start;
     for (size_t i = 0; i < tensors.size(); ++i)
     {
         TensorInfo &t = tensors[i];
-        uint64_t n = t.ne[0] * t.ne[1] * t.ne[2] * t.ne[3];
-        if (t.type == GGML_F32)
-            t.bytes = n * 4;
-        else if (t.type == GGML_F16)
-            t.bytes = n * 2;
+        if (t.offset > data_size)
+        {
+            *err = "tensor offset past end of file: " + t.name;
+            return false;
+        }
+        const uint64_t room = data_size - t.offset; // bytes from the tensor's start to the end of the file
+        uint64_t n = 1;
+        for (int d = 0; d < 4; ++d)
+        {
+            if (t.ne[d] != 0 && n > UINT64_MAX / t.ne[d])
+            {
+                *err = "tensor element count overflows: " + t.name;
+                return false;
+            }
+            n *= t.ne[d];
+        }
+        if (t.type == GGML_F32 || t.type == GGML_F16)
+        {
+            const uint64_t es = t.type == GGML_F32 ? 4 : 2;
+            if (n > room / es)
+            {
+                *err = "tensor data past end of file: " + t.name;
+                return false;
+            }
+            t.bytes = n * es;
+        }
         else
         {
             // other encodings: the span up to the next tensor (or the end of the file)
-            uint64_t next = size - data_start;
+            uint64_t next = data_size;
             for (const TensorInfo &o : tensors)
                 if (o.offset > t.offset && o.offset < next)
                     next = o.offset;
             t.bytes = next - t.offset;
-        }
-        if (data_start + t.offset + t.bytes > size)
-        {
-            *err = "tensor data past end of file: " + t.name;
-            return false;
         }
         t.data = base + data_start + t.offset;
     }

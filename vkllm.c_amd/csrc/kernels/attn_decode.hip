@@ -221,7 +221,6 @@ __global__ __launch_bounds__(256) void attn_pvc_kernel(AttnDecodeArgs a)
 // of the head has counted before it reduces them. The partial sums are then merged as in attn_pvc_kernel, on the
 // same counter (a second round of arrivals); the merging block clears it. The launcher admits the launch only when
 // every block can be resident at once.
-constexpr uint32_t kLongSpinLimit = 1u << 20;
 
 __global__ __launch_bounds__(256) void attn_long_kernel(AttnDecodeArgs a)
 {
@@ -274,10 +273,10 @@ __global__ __launch_bounds__(256) void attn_long_kernel(AttnDecodeArgs a)
         __hip_atomic_store(st + 2 * c + 1, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_s_waitcnt(0);
         __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        uint32_t spins = 0, failed = 0;
-        while (__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < nc)
+        uint32_t spins = 0, failed = a.spin_limit == 0 ? 1u : 0u;
+        while (!failed && __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < nc)
         {
-            if (++spins >= kLongSpinLimit)
+            if (++spins >= a.spin_limit)
             {
                 failed = 1;
                 break;
@@ -546,7 +545,6 @@ __global__ __launch_bounds__(kSmallThreads) void attn_decode_small_kernel(AttnDe
 //     out[r] = fp16(resid[r] + fp16(Wo[r] . attn)). The last of these blocks to finish clears the counters.
 // Attention blocks never wait, and the launcher sizes the grid so that every block is resident at once. A wait that
 // gives up sets *err (the step's outputs are then not valid).
-constexpr uint32_t kSpinLimit = 1u << 18;
 // sync words: arrival counters at kSyncStride c (c < 8), then top, ready and done, each on its own 256 bytes
 constexpr uint32_t kSyncStride = 64;
 constexpr uint32_t kSyncTop = 8 * kSyncStride, kSyncReady = 9 * kSyncStride, kSyncDone = 10 * kSyncStride;
@@ -602,10 +600,10 @@ template <int NV> __global__ __launch_bounds__(kSmallThreads, 4) void attn_o_ker
     load_unit(u);
     if (tid == 0)
     {
-        uint32_t spins = 0, failed = 0;
-        while (__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u)
+        uint32_t spins = 0, failed = a.at.spin_limit == 0 ? 1u : 0u;
+        while (!failed && __hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0u)
         {
-            if (++spins >= kSpinLimit)
+            if (++spins >= a.at.spin_limit)
             {
                 failed = 1;
                 break;
@@ -703,7 +701,7 @@ hipError_t launch_attn_long(hipStream_t st, const AttnDecodeArgs &a, int cu_coun
     // one round trip of keys and of V rows per block (head_dim <= 128 with chunks of <= 256 positions); the
     // transposed product (kv == hd) fits one chunk
     if (!attn_args_ok(a) || a.hd > 128 || a.cmax == 0 || a.chunk == 0 || a.chunk > 256 || a.chunk < a.hd ||
-        (uint64_t)a.chunk * a.cmax < a.ctx || !a.part || !a.stats || !a.long_sync || !a.err)
+        (uint64_t)a.chunk * a.cmax < a.ctx || a.cmax > 256 || !a.part || !a.stats || !a.long_sync || !a.err)
         return hipErrorInvalidValue;
     const size_t lds = (size_t)a.chunk * sizeof(float);
     static size_t cached_lds = 0;

@@ -21,7 +21,7 @@ namespace vk
 {
 
 // ---------------------------------------------------------------------------------------------------------------
-// EMBEDDING (src/shaders/vkllm_embedding.comp:138-167) for contiguous rows
+// EMBEDDING (src/shaders/vkllm_embedding.comp:41-70) for contiguous rows
 __global__ void embed_rows_kernel(const uint32_t *toks, const uint16_t *embd, uint16_t *h, uint32_t V, uint32_t D,
                                   uint32_t unk)
 {
@@ -736,7 +736,7 @@ hipError_t launch_attn_prefill(hipStream_t st, const uint16_t *q, const uint16_t
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// RoPE (normal style, src/shaders/vkllm_rope.comp:146-174) on q and k of a prefill QKV block, k and v appended to
+// RoPE (normal style, src/shaders/vkllm_rope.comp:39-79) on q and k of a prefill QKV block, k and v appended to
 // the caches (src/shaders/vkllm_update_rows.comp:21-46)
 __global__ void rope_kv_kernel(const uint16_t *qkv, uint16_t *q, uint16_t *kc, uint16_t *vc, const float *freqs,
                                uint32_t offset, uint32_t S, uint32_t D, uint32_t hd, uint32_t ctx)

@@ -117,8 +117,14 @@ struct AttnDecodeArgs
     // kernel leaves them zero), and the flag it sets (system scope) when a wait gives up
     uint32_t *long_sync;
     uint32_t *err;
+    // polls a bounded wait makes before it gives up (the one-kernel long-cache attention and the attention +
+    // projection launch); 0 gives up at once, without polling, so the failure path can be forced from the host
+    uint32_t spin_limit;
 };
 constexpr uint32_t kAttnLongStride = 64;
+// default spin limits of the bounded waits: each poll sleeps ~64 clocks, so these are ~0.5 s and ~0.1 s
+constexpr uint32_t kAttnLongSpinLimit = 1u << 20;
+constexpr uint32_t kAttnOSpinLimit = 1u << 18;
 // dim slices per head: the largest divisor of hd / 8 up to max_groups with H * groups <= 1024
 uint32_t attn_groups(uint32_t H, uint32_t hd, uint32_t max_groups);
 hipError_t launch_attn_scores(hipStream_t st, const AttnDecodeArgs &a);

@@ -91,7 +91,7 @@ hipError_t launch_bin(hipStream_t st, const TView &a, const TView &b, const TVie
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// VKLLM_OP_EMBEDDING (src/shaders/vkllm_embedding.comp:138-167): one workgroup per index; index (0, c, h, w)
+// VKLLM_OP_EMBEDDING (src/shaders/vkllm_embedding.comp:41-70): one workgroup per index; index (0, c, h, w)
 // writes output row c*s0 + h*s1 + w*s2; ids >= rows read row `unk`.
 __global__ void embedding_kernel(TView idx, TView table, TView out, uint32_t unk)
 {
@@ -242,7 +242,7 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(TView a, TView b0, TV
         }
 }
 
-// M == 1 with B [N, K] (the reference's mat_mul_vec case, src/shaders/vkllm_mat_mul_vec.comp:115-171): one wave per
+// M == 1 with B [N, K] (the reference's mat_mul_vec case, src/shaders/vkllm_mat_mul_vec.comp:94-150): one wave per
 // output element, lanes striding K.
 __global__ __launch_bounds__(256) void gemv_generic_kernel(TView a, TView b, TView out, float scale, int act)
 {

@@ -7,6 +7,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <string>
+#include <unordered_set>
 #include <vector>
 
 #include "gguf.h"
@@ -422,7 +423,7 @@ static vkllm_err_t load_standalone(vkllm_context *ctx, vkllm_models_llama2 *m, c
             slot = &m->weights.output_norm_weight;
         else if (t.name == "output.weight")
             slot = &m->weights.output_weight;
-        else if (sscanf(t.name.c_str(), "blk.%u.%95s", &l, rest) == 2)
+        else if (sscanf(t.name.c_str(), "blk.%u.%95s", &l, rest) == 2 && l < m->meta.block_count)
         {
             while (m->weights.blocks->used_n <= l)
                 vkllm_array_block_weights_append(m->weights.blocks,
@@ -456,6 +457,38 @@ static vkllm_err_t load_standalone(vkllm_context *ctx, vkllm_models_llama2 *m, c
 }
 
 extern "C" vkllm_err_t vkllm_models_llama2_free(struct vkllm_context *context, struct vkllm_models_llama2 *model);
+
+// Every weight the graph reads was found in the file. The reference leaves a missing one NULL and the graph build
+// then dereferences it; here the load fails instead and names the first missing tensor.
+static bool all_weights_present(const vkllm_models_llama2 *m, const char *file)
+{
+    const char *missing = nullptr;
+    unsigned layer = 0;
+    if (!m->weights.tok_embed_weights)
+        missing = "token_embd.weight";
+    else if (!m->weights.output_norm_weight)
+        missing = "output_norm.weight";
+    else if (!m->weights.output_weight)
+        missing = "output.weight";
+    for (uint32_t l = 0; !missing && m->weights.blocks && l < m->weights.blocks->used_n; ++l)
+    {
+        const block_weights *b = m->weights.blocks->data[l];
+        layer = l;
+        if (!b->attn_norm_weight)
+            missing = "attn_norm.weight";
+        else if (!b->ffn_norm_weight)
+            missing = "ffn_norm.weight";
+        else if (!b->WQ || !b->WK || !b->WV || !b->WO)
+            missing = "an attention weight";
+        else if (!b->WU || !b->WG || !b->WD)
+            missing = "an ffn weight";
+    }
+    if (!missing && (!m->weights.blocks || m->weights.blocks->used_n != m->meta.block_count))
+        missing = "a block";
+    if (missing)
+        log_error("gguf %s lacks %s (block %u)", file, missing, layer);
+    return missing == nullptr;
+}
 
 extern "C" vkllm_err_t vkllm_models_llama2_load(struct vkllm_context *context, struct vkllm_models_llama2 *model,
                                                 const char *file)
@@ -492,7 +525,9 @@ extern "C" vkllm_err_t vkllm_models_llama2_load(struct vkllm_context *context, s
         mp->L = model->meta.block_count;
         // every expected tensor must be present with its slab shape and type
         size_t expected = 9 * (size_t)mp->L + 3, matched = 0;
-        std::vector<bool> seen;
+        // slab regions already claimed: a name repeated in the file must not count twice (its region would be
+        // written twice while another one stayed uninitialised)
+        std::unordered_set<const void *> claimed;
         vkllm_err_t rc = build_slabs(context, model, mp);
         if (rc != VKLLM_ERR_OK)
         {
@@ -508,7 +543,7 @@ extern "C" vkllm_err_t vkllm_models_llama2_load(struct vkllm_context *context, s
             if (t.n_dims > 2)
                 continue;
             void *d = slab_dst(mp, model, t, rows, cols, false);
-            if (d)
+            if (d && claimed.insert(d).second)
             {
                 dst[i] = d;
                 matched++;
@@ -560,6 +595,8 @@ extern "C" vkllm_err_t vkllm_models_llama2_load(struct vkllm_context *context, s
     if (!slabbed)
     {
         vkllm_err_t rc = load_standalone(context, model, f);
+        if (rc == VKLLM_ERR_OK && !all_weights_present(model, file))
+            rc = VKLLM_ERR_ARGS;
         if (rc != VKLLM_ERR_OK)
         {
             vkllm_models_llama2_free(context, model);

@@ -162,7 +162,7 @@ extern "C" vkllm_err_t vkllm_op_embedding_init(struct vkllm_context *context, st
         return VKLLM_ERR_ARGS;
     if (tensor->dtype != table->dtype)
         return VKLLM_ERR_PIPELINE_NOT_FOUND;
-    // index (0, c, h, w) writes output row (c, h, w) (src/shaders/vkllm_embedding.comp:160); keep it in bounds
+    // index (0, c, h, w) writes output row (c, h, w) (src/shaders/vkllm_embedding.comp:63); keep it in bounds
     _CHECK_ARGS(tensor->shapes[0] >= idx->shapes[1] && tensor->shapes[1] >= idx->shapes[2] &&
                 tensor->shapes[2] >= idx->shapes[3] && tensor->shapes[3] >= table->shapes[3]);
     tensor->pipeline = pipeline_of(context, KID_EMBEDDING);
@@ -343,7 +343,7 @@ extern "C" vkllm_err_t vkllm_op_rope_run(struct vkllm_context *context, struct v
     const uint32_t D = tensor->srcs[0]->shapes[3];
     float freqs[vk::kMaxRopeFreqs];
     for (uint32_t w = 0; w < D / 2; ++w)
-        freqs[w] = powf(p.base, (float)(2 * w) / (float)D); // base^(2w/D), src/shaders/vkllm_rope.comp:164
+        freqs[w] = powf(p.base, (float)(2 * w) / (float)D); // base^(2w/D), src/shaders/vkllm_rope.comp:68
     vk::TView in = tview(context, tensor->srcs[0]), out = tview(context, tensor);
     NEED_DEV(in);
     NEED_DEV(out);
