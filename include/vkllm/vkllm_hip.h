@@ -97,6 +97,18 @@ extern vkllm_err_t vkllm_hip_gemm(struct vkllm_context *context, int epi, const 
                                   uint16_t *C, uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split,
                                   float *work, uint64_t work_elems);
 
+/* vkllm_hip_gemm for callers that cannot allocate device memory (code under stream capture, serving loops that
+ * forbid hipMalloc). It has no counterpart in the reference. The split-K partial tiles go to a fixed scratch array
+ * of the library (8M floats, 32 MiB, held by every GPU the library runs on until the process ends) instead of a
+ * caller buffer: `work_elems` (at most 8M, else VKLLM_ERR_ARGS) is how much of it the product may use, with the
+ * meaning of vkllm_hip_gemm's work_elems, so the same arguments give the same tile and split choices and identical
+ * results. The call enqueues on the context's stream and returns without waiting (vkllm_hip_synchronize waits); it
+ * calls no allocating routine. Calls queued on one stream run in order; calls from two contexts on one GPU at once
+ * race on the shared scratch. */
+extern vkllm_err_t vkllm_hip_gemm_noalloc(struct vkllm_context *context, int epi, const uint16_t *A,
+                                          const uint16_t *B, uint16_t *C, uint32_t M, uint32_t N, uint32_t K,
+                                          uint32_t ldc, uint32_t split, uint64_t work_elems);
+
 /* Synchronise the context's stream. */
 extern vkllm_err_t vkllm_hip_synchronize(struct vkllm_context *context);
 

@@ -349,6 +349,12 @@ extern "C" vkllm_err_t vkllm_context_new(uint32_t dev, struct vkllm_context **co
         return VKLLM_ERR_DEV_NOT_FOUND;
     }
     HIP_TRY(hipSetDevice((int)dev));
+    // the allocation-free GEMM's scratch array: its address on this device, looked up once with the device current
+    {
+        const hipError_t e = vk::noalloc_scratch_init((int)dev);
+        if (e != hipSuccess)
+            return hip_fail(e, "hipGetSymbolAddress(scratch)", __FILE__, __LINE__);
+    }
     // host waits on the stream spin rather than sleep: a token step is milliseconds long and waking a sleeping
     // waiter adds tens of microseconds to every step (VKLLM_SPIN_WAIT=0 keeps HIP's default scheduling)
     if (env_flag("VKLLM_SPIN_WAIT", 1) && hipSetDeviceFlags(hipDeviceScheduleSpin) != hipSuccess)

@@ -209,6 +209,9 @@ struct GemmNorm
 hipError_t launch_gemm(hipStream_t st, int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, uint32_t M,
                        uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, int cu_count, float *work,
                        size_t work_elems, const GemmRope *rope = nullptr, const GemmNorm *norm = nullptr);
+// Looks up the device address of the allocation-free GEMM's scratch array on device `dev` (current), once per
+// device; vkllm_context_new calls it.
+hipError_t noalloc_scratch_init(int dev);
 // cs[s][w] = (cos f, sin f) with f = (offset + s) / freqs[w], s < S, w < hd / 2 (the angles launch_rope_kv uses)
 hipError_t launch_rope_table(hipStream_t st, float *cs, const float *freqs, uint32_t offset, uint32_t S,
                              uint32_t hd);
