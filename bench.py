@@ -22,8 +22,8 @@ Printed (one JSON line on stdout):
                library's stream, and its algorithmic GB/s
   roofline     the dominant decode kernel (the fused RMSNorm + gate/up GEMV + SwiGLU): algorithmic bytes per
                launch / its average duration over back-to-back launches across all layers' weights
-  cpu_baseline the C oracle (scalar, double accumulation) timing a decode step of a 2-layer slice of the same
-               shape, scaled to the full depth by multiply-accumulate count
+  cpu_baseline the C oracle (the CPU restatement of the reference's graph, double accumulation) timing greedy
+               decode steps of the full-depth model on the host's cores (at most 16 threads)
 """
 import argparse
 import json
@@ -77,6 +77,20 @@ def decode_bytes(shape, kv):
     }
 
 
+def decode_families(shape, kv):
+    """The kernel families a decode step at `kv` positions runs with the library's defaults and this process's
+    VKLLM_* switches: the one-kernel short-cache attention (kv <= ATTN_SMALL_MAX; with Wo in the same launch under
+    VKLLM_ATTN_O=1), or the long-cache attention (one launch, or scores + P.V under VKLLM_ATTN_LONG=0)."""
+    env = os.environ.get
+    small_max = int(env("VKLLM_ATTN_SMALL_MAX", str(ATTN_SMALL_MAX)))
+    fam = ["fused_embed", "fused_qkv_rope", "fused_gateup", "fused_down_resid", "fused_logits", "fused_argmax"]
+    if kv <= small_max:
+        return fam + (["fused_attn_o"] if env("VKLLM_ATTN_O", "0") == "1" else ["fused_attn_small", "fused_o_resid"])
+    if env("VKLLM_ATTN_LONG", "1") == "0":
+        return fam + ["fused_attn_scores", "fused_attn_pv", "fused_o_resid"]
+    return fam + ["fused_attn_long", "fused_o_resid"]
+
+
 def step_bytes(shape, kv):
     """Whole decode step at `kv` positions: the per-layer kernels times the depth, plus embed, logits, arg max."""
     b = decode_bytes(shape, kv)
@@ -112,16 +126,25 @@ def copy_calibration(ctx, vk, mib):
     log(f"copy calibration: 4 copies of {mib} MiB")
 
 
+def oracle_threads():
+    """Threads the oracle's parallel loops use (its rule: ORACLE_THREADS, else the online CPUs, at most 16)."""
+    n = int(os.environ.get("ORACLE_THREADS", "0") or 0) or (os.cpu_count() or 1)
+    return max(1, min(16, n))
+
+
 def cpu_baseline(shape, seconds):
-    """Decode tokens/s of the C oracle on one host core. The sample is decode steps of a 2-layer model of the
-    same widths from an empty cache, timed until `seconds` have passed, scaled to the full depth by
-    multiply-accumulate count (matmuls are > 99% of the oracle's work)."""
+    """Decode tokens/s of the C oracle (the CPU restatement of the reference's graph: fp16 storage, double
+    accumulation) at the workload's full depth on the host's cores. The model is built first (not timed); the sample
+    is greedy decode steps from an empty cache until `seconds` have passed (attention over a short cache is under 1%
+    of a step's work at these widths, so the cache length does not change the rate)."""
     sys.path.insert(0, os.path.join(HERE, "oracle"))
     import oracle_ffi as oracle
 
-    D, F, V = shape["dim"], shape["ffn"], shape["vocab"]
-    cfg = oracle.make_cfg(2, D, shape["n_head"], F, vocab=V, ctx=64)
+    D, F, V, L = shape["dim"], shape["ffn"], shape["vocab"], shape["n_layer"]
+    t_build = time.perf_counter()
+    cfg = oracle.make_cfg(L, D, shape["n_head"], F, vocab=V, ctx=64)
     m = oracle.Model(cfg=cfg, seed=MODEL_SEED)
+    t_build = time.perf_counter() - t_build
     try:
         tok = [int(oracle.prompt_tokens(PROMPT_SEED, 1, V)[0])]
         n, t0 = 0, time.perf_counter()
@@ -130,20 +153,19 @@ def cpu_baseline(shape, seconds):
             tok = [int(ids[-1])]
             n += 1
             el = time.perf_counter() - t0
-            if el >= seconds or n >= 60:
+            if (el >= seconds and n >= 2) or n >= 60:
                 break
     finally:
         m.close()
-    mac_layer = 4 * D * D + 3 * D * F
-    scale = (shape["n_layer"] * mac_layer + V * D) / (2 * mac_layer + V * D)
-    per_token = el / n * scale
+    cores = oracle_threads()
     return {
-        "value": round(1.0 / per_token, 5),
+        "value": round(n / el, 4),
         "unit": "tok/s",
-        "cores": 1,
+        "cores": cores,
         "kind": "port",
-        "sample": f"{n} decode steps of a 2-layer dim-{D}/FFN-{F}/vocab-{V} slice in {el:.1f} s on one core, "
-                  f"x{scale:.2f} by MAC count to {shape['n_layer']} layers",
+        "sample": f"{n} greedy decode steps of the full {L}-layer dim-{D}/FFN-{F}/vocab-{V} model (positions 0-{n - 1}) "
+                  f"in {el:.1f} s on {cores} host threads; model built from seed {MODEL_SEED} in {t_build:.0f} s "
+                  f"(not timed)",
     }
 
 
@@ -155,7 +177,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=None, help="untimed decode steps before the timed ones")
     ap.add_argument("--prefill-reps", type=int, default=4, help="timed prompt prefills")
     ap.add_argument("--timing-steps", type=int, default=32, help="graph replays timed for the device-only rate")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline sample length (0: skip)")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample length (0: skip)")
     ap.add_argument("--ctx", type=int, default=None, help="KV cache positions (default: the workload's)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first run the COPY op on MIB MiB (reference kernel for rocprofv3 byte counters)")
@@ -231,50 +253,27 @@ def main():
 
     # per-kernel durations: back-to-back launches between one hipEvent pair on the library's stream
     nbytes = decode_bytes(shape, pos)
+    used = decode_families(shape, pos)
     kernels = {}
     step_kernel_ns = 0.0
-    small_attn = pos <= ATTN_SMALL_MAX  # the library's default switch-over to the two-kernel attention
-    # short caches: attention and the output projection run as one launch with VKLLM_ATTN_O=1
-    attn_o = small_attn and os.environ.get("VKLLM_ATTN_O", "0") == "1"
-    # long caches: scores and P.V in one launch when the device holds every chunk block at once (the library then
-    # uses it; it refuses to time it otherwise)
-    attn_long = False
-    for name in ("fused_embed", "fused_qkv_rope", "fused_attn_o", "fused_attn_small", "fused_attn_long",
-                 "fused_attn_scores", "fused_attn_pv", "fused_o_resid", "fused_gateup", "fused_down_resid",
-                 "fused_logits", "fused_argmax"):
+    for name in ("fused_embed", "fused_qkv_rope", "fused_attn_o", "fused_attn_small",
+                 "fused_attn_long", "fused_attn_scores", "fused_attn_pv", "fused_o_resid", "fused_gateup",
+                 "fused_down_resid", "fused_logits", "fused_argmax"):
         per_layer = name not in ("fused_embed", "fused_logits", "fused_argmax")
         reps = 4 * L if per_layer else 32
-        if name in ("fused_attn_o", "fused_attn_small") and pos > ATTN_SMALL_MAX:
-            continue  # the one-kernel attention takes at most ATTN_SMALL_MAX positions
-        if name == "fused_attn_long":
-            if small_attn or os.environ.get("VKLLM_ATTN_LONG", "1") == "0":
-                continue
-            try:
-                avg_ns = model.time_kernel(name, reps)
-            except vk.VkllmError:
-                continue
-            attn_long = True
-        elif name == "fused_attn_o" and not attn_o:
-            try:  # optional kernel: the device may not hold its two parts at once for this shape
-                avg_ns = model.time_kernel(name, reps)
-            except vk.VkllmError:
-                continue
-        else:
+        try:  # kernels outside the step's variant are timed where the library takes this cache length
             avg_ns = model.time_kernel(name, reps)
-        if attn_long and name in ("fused_attn_scores", "fused_attn_pv"):
-            used = False
-        elif attn_o:
-            used = name not in ("fused_attn_small", "fused_attn_scores", "fused_attn_pv", "fused_o_resid")
-        else:
-            used = name != "fused_attn_o" and not ((name == "fused_attn_small" and not small_attn) or
-                                                   (name in ("fused_attn_scores", "fused_attn_pv") and small_attn))
-        if used:
+        except vk.VkllmError:
+            if name in used:
+                raise
+            continue
+        if name in used:
             step_kernel_ns += avg_ns * (L if per_layer else 1)
-        row = {"avg_us": round(avg_ns / 1e3, 3)}
+        row = {"avg_us": round(avg_ns / 1e3, 3), "in_step": name in used}
         if name in nbytes:
             row["GBps"] = round(nbytes[name] / avg_ns, 1)
         kernels[name] = row
-        log(f"  {name:20s} avg {avg_ns / 1e3:9.2f} us  {row.get('GBps', '')}")
+        log(f"  {name:20s} avg {avg_ns / 1e3:9.2f} us  {row.get('GBps', ''):>8}  {'step' if name in used else ''}")
     dom = "fused_gateup"
     dom_avg_ns = kernels[dom]["avg_us"] * 1e3
     achieved = nbytes[dom] / dom_avg_ns  # GB/s
@@ -314,7 +313,7 @@ def main():
     model.close()
     ctx.close()
     if args.cpu_seconds > 0:
-        log("cpu baseline (oracle, one core)")
+        log(f"cpu baseline (oracle, full depth, {oracle_threads()} threads)")
         result["cpu_baseline"] = cpu_baseline(shape, args.cpu_seconds)
     else:
         result["cpu_baseline"] = None
