@@ -26,6 +26,10 @@ struct FusedPlan
     uint32_t S;
 };
 
+// Short-cache decode steps are captured per bucket of kSmallBucket cache positions: a bucket's launches bound their
+// LDS and the keys and V rows they request before the position is known by the bucket's end.
+constexpr uint32_t kSmallBucket = 128, kSmallBuckets = 12;
+
 struct FusedState
 {
     uint32_t cap_S = 0; // rows the activation buffers hold
@@ -61,9 +65,13 @@ struct FusedState
     bool norm_epi = true;
     // polls of the bounded waits before they give up (VKLLM_SPIN_LIMIT; 0 forces the give-up path)
     uint32_t long_spin_limit = vk::kAttnLongSpinLimit, attn_o_spin_limit = vk::kAttnOSpinLimit;
-    // captured single-token steps: [0] with the one-kernel attention, [1] with the two-kernel attention
-    hipGraph_t graph[2] = {nullptr, nullptr};
-    hipGraphExec_t exec[2] = {nullptr, nullptr};
+    // captured single-token steps, one per attention variant: [b] (b < kSmallBuckets) the one-kernel attention for
+    // caches of at most (b + 1) * kSmallBucket positions (the launch's bound for its LDS and speculative loads),
+    // [kSmallBuckets] the long-cache attention
+    hipGraph_t graph[kSmallBuckets + 1] = {};
+    hipGraphExec_t exec[kSmallBuckets + 1] = {};
+    // the positions bound of the short-cache launches being enqueued (the current variant's)
+    uint32_t small_kv_max = 0;
     int last_exec = -1;
     // VKLLM_TRACE_HOST=1: host time of single-token steps spent enqueueing and waiting, printed at release
     bool trace = false;
@@ -111,7 +119,7 @@ static void free_buffers(FusedState *fs)
 
 static void drop_graphs(FusedState *fs)
 {
-    for (int i = 0; i < 2; ++i)
+    for (uint32_t i = 0; i <= kSmallBuckets; ++i)
     {
         if (fs->exec[i])
             (void)hipGraphExecDestroy(fs->exec[i]);
@@ -188,6 +196,7 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         shape.groups = vk::attn_groups(mp->H, mp->hd, fs->attn_max_groups);
         const uint32_t limit = vk::attn_small_limit(shape);
         small = small < limit ? small : limit;
+        small = small < kSmallBucket * kSmallBuckets ? small : kSmallBucket * kSmallBuckets;
         fs->attn_small_max = small < mp->ctx ? small : mp->ctx;
         const char *ao = getenv("VKLLM_ATTN_O");
         fs->attn_o = ao && *ao == '1';
@@ -311,7 +320,7 @@ static hipError_t launch_decode_kernel(vkllm_context *ctx, ModelPriv *mp, Kernel
         if (kid == KID_F_ATTN_LONG)
             return vk::launch_attn_long(st, at, cu);
         if (kid == KID_F_ATTN_SMALL)
-            return vk::launch_attn_small(st, at, fs->attn_small_max);
+            return vk::launch_attn_small(st, at, fs->small_kv_max);
         if (kid == KID_F_ATTN_O)
         {
             // attention, then h + Wo attn in the same launch
@@ -322,7 +331,7 @@ static hipError_t launch_decode_kernel(vkllm_context *ctx, ModelPriv *mp, Kernel
             ao.out = resid_out ? resid_out : fs->h;
             ao.sync = fs->attn_sync;
             ao.err = &fs->dio->err;
-            return vk::launch_attn_o(st, ao, fs->attn_small_max, cu);
+            return vk::launch_attn_o(st, ao, fs->small_kv_max, cu);
         }
         return kid == KID_F_ATTN_SCORES ? vk::launch_attn_scores(st, at) : vk::launch_attn_pv(st, at);
     }
@@ -363,9 +372,23 @@ static hipError_t launch_decode_kernel(vkllm_context *ctx, ModelPriv *mp, Kernel
 
 #define DTRY(_ctx, _mp, _kid, _l) KTRY(_ctx, _kid, launch_decode_kernel((_ctx), (_mp), (_kid), (_l)))
 
-// decode: S == 1, position from fs->step; `small_attn` picks the one-kernel attention (kv <= attn_small_max)
-static vkllm_err_t enqueue_decode(vkllm_context *ctx, ModelPriv *mp, bool small_attn)
+// the attention variant of a single-token step at cache length kv: the short-cache bucket b < kSmallBuckets, or
+// kSmallBuckets for the long-cache path
+static uint32_t decode_variant(const FusedState *fs, uint32_t kv)
 {
+    return kv <= fs->attn_small_max ? (kv - 1) / kSmallBucket : kSmallBuckets;
+}
+
+// decode: S == 1, position from fs->step; `variant` (decode_variant) picks the attention kernels and, for short caches,
+// the positions bound of their launches
+static vkllm_err_t enqueue_decode(vkllm_context *ctx, ModelPriv *mp, uint32_t variant)
+{
+    const bool small_attn = variant < kSmallBuckets;
+    if (small_attn)
+    {
+        const uint32_t end = (variant + 1) * kSmallBucket;
+        mp->fs->small_kv_max = end < mp->fs->attn_small_max ? end : mp->fs->attn_small_max;
+    }
     DTRY(ctx, mp, KID_F_EMBED, 0);
     for (uint32_t l = 0; l < mp->L; ++l)
     {
@@ -488,17 +511,16 @@ vkllm_err_t fused_plan_init(vkllm_context *ctx, vkllm_graph *graph)
 
 // Enqueues one single-token step: a replay of the captured graph for this attention variant (captured on first
 // use), or direct launches when graph replay or timing says so.
-static vkllm_err_t launch_decode_step(vkllm_context *ctx, ModelPriv *mp, bool small)
+static vkllm_err_t launch_decode_step(vkllm_context *ctx, ModelPriv *mp, uint32_t v)
 {
     FusedState *fs = mp->fs;
     hipStream_t st = ctx->device->stream;
     if (!ctx->device->graph_replay || ctx->device->timing)
-        return enqueue_decode(ctx, mp, small);
-    const int v = small ? 0 : 1;
+        return enqueue_decode(ctx, mp, v);
     if (!fs->exec[v])
     {
         HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
-        vkllm_err_t rc = enqueue_decode(ctx, mp, small);
+        vkllm_err_t rc = enqueue_decode(ctx, mp, v);
         hipGraph_t g = nullptr;
         hipError_t ce = hipStreamEndCapture(st, &g);
         if (rc != VKLLM_ERR_OK)
@@ -535,8 +557,8 @@ vkllm_err_t fused_plan_run(vkllm_context *ctx, vkllm_graph *graph)
         fs->dio->token = toks[0];
         fs->dio->err = 0;
         const uint64_t t0 = fs->trace ? host_ns() : 0;
-        const bool small = p->offset + 1 <= fs->attn_small_max;
-        _CHECK(launch_decode_step(ctx, mp, small));
+        const uint32_t variant = decode_variant(fs, p->offset + 1);
+        _CHECK(launch_decode_step(ctx, mp, variant));
         const uint64_t t1 = fs->trace ? host_ns() : 0;
         HIP_TRY(hipStreamSynchronize(st));
         if (((volatile vk::DecodeIo *)fs->dio)->err)
@@ -555,7 +577,7 @@ vkllm_err_t fused_plan_run(vkllm_context *ctx, vkllm_graph *graph)
             fs->attn_long = false;
             fs->attn_o = false;
             fs->dio->err = 0;
-            _CHECK(launch_decode_step(ctx, mp, small));
+            _CHECK(launch_decode_step(ctx, mp, variant));
             HIP_TRY(hipStreamSynchronize(st));
             if (((volatile vk::DecodeIo *)fs->dio)->err)
                 return VKLLM_ERR_VULKAN;
@@ -645,6 +667,13 @@ extern "C" vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *ctx, st
         log_error("%s takes at most %u positions; the last step had %u", family, fs->attn_small_max,
                   fs->dio->offset + 1);
         return VKLLM_ERR_ARGS;
+    }
+    if (kid == KID_F_ATTN_SMALL || kid == KID_F_ATTN_O)
+    {
+        // the launches of the last step's bucket
+        const uint32_t b = decode_variant(fs, fs->dio->offset + 1);
+        const uint32_t end = (b + 1) * kSmallBucket;
+        fs->small_kv_max = end < fs->attn_small_max ? end : fs->attn_small_max;
     }
     hipStream_t st = ctx->device->stream;
     // the residual GEMVs write into fs->xn (a scratch row) so that repeating them leaves the model state unchanged

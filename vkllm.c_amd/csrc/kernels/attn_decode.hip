@@ -409,16 +409,18 @@ __device__ __forceinline__ void pv_transposed_pairs(const float *pl, const uint1
 // Block (h, g) of the short-cache attention: all kv keys of head h scored, the softmax statistics, then the
 // probability-weighted sum of dims [g dg, (g + 1) dg) of V.
 // The first two batches of keys and two passes of V rows (512 positions at head_dim 128) are requested before the
-// position is known, at rows clamped to the cache (further V passes follow the keys); rows at or past kv never reach a score or a sum (their scores are
-// not stored and their V values are replaced by zeros, whatever the cache holds there). After the scores are in
-// LDS every wave reduces the statistics itself, so no further exchange is needed until the P.V partials.
+// position is known, at rows clamped to the launch's largest cache length small_max (further V passes follow the
+// keys): a launch for short caches asks HBM for no row past small_max, the clamped requests repeat a row already in
+// flight. Rows at or past kv never reach a score or a sum (their scores are not stored and their V values are
+// replaced by zeros, whatever the cache holds there). After the scores are in LDS every wave reduces the statistics
+// itself, so no further exchange is needed until the P.V partials.
 template <int NT, bool AGENT>
 __device__ __forceinline__ void small_block(const AttnDecodeArgs &a, uint32_t h, uint32_t g, float *sm, float *red)
 {
     constexpr uint32_t NW = NT / 64;
     constexpr int U = 4, UV = kSmallMaxPasses;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t dg = a.hd / a.groups, d0 = g * dg, vpr = a.hd / 8, last = a.ctx - 1;
+    const uint32_t dg = a.hd / a.groups, d0 = g * dg, vpr = a.hd / 8, last = min(a.small_max, a.ctx) - 1;
     // V layout: lane = (vector vl of the slice, row slot); a wave covers seg rows, the block rpp rows per pass
     const uint32_t lpr = dg / 8, seg = 64 / lpr;
     const uint32_t vl = lane / seg, vs = wave * seg + lane % seg, rpp = NW * seg;
@@ -513,14 +515,22 @@ __device__ __forceinline__ void small_block(const AttnDecodeArgs &a, uint32_t h,
     }
 }
 
-// block b of the short-cache attention (blocks of heads >= H, and launches past the LDS's positions, do nothing)
+// block b of the short-cache attention (blocks of heads >= H do nothing). A position past the launch's small_max
+// (the LDS's positions and the speculative loads' bound) is a host error: the block raises the step's error flag
+// and writes nothing.
 template <bool AGENT> __device__ __forceinline__ void small_attention(const AttnDecodeArgs &a, uint32_t b, float *sm,
                                                                      float *red)
 {
     uint32_t h, g;
     block_head(b, a.groups, h, g);
-    if (h >= a.H || a.step->offset + 1 > a.small_max)
+    if (h >= a.H)
         return;
+    if (a.step->offset + 1 > a.small_max)
+    {
+        if (threadIdx.x == 0 && a.err)
+            __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        return;
+    }
     small_block<kSmallThreads, AGENT>(a, h, g, sm, red);
 }
 
