@@ -27,29 +27,74 @@ def np_of(dt):
 
 
 # ---------------------------------------------------------------------------------------------------------------
-# MATMUL: tests/vkllm_test_op_matmul.c:179-286 (B_a, C_a, B_b, C_b, M, K, N, dtype, transposed_b, act)
+# MATMUL: every case of tests/vkllm_test_op_matmul.c:179-286 in its order (B_a, C_a, B_b, C_b, M, K, N, dtype,
+# transposed_b, act), then the token step's decode shapes
 MATMUL_CASES = [
     (1, 1, 1, 1, 1, 1024, 2048, "f32", True, False),
     (1, 1, 1, 1, 1, 1024, 2048, "f16", True, False),
     (1, 1, 1, 1, 512, 1024, 2048, "f16", True, False),
     (1, 1, 1, 1, 333, 1259, 365, "f16", True, False),
+    (1, 1, 1, 1, 512, 1024, 2048, "f32", True, False),
     (1, 1, 1, 1, 333, 1259, 365, "f32", True, False),
     (1, 1, 1, 1, 512, 1024, 2048, "f16", False, False),
+    (1, 1, 1, 1, 333, 1259, 365, "f16", False, False),
+    (1, 1, 1, 1, 512, 1024, 2048, "f32", False, False),
     (1, 1, 1, 1, 333, 1259, 365, "f32", False, False),
     (4, 1, 4, 1, 256, 512, 1024, "f16", True, False),
+    (8, 1, 8, 1, 128, 256, 512, "f32", True, False),
+    (16, 1, 16, 1, 64, 128, 256, "f16", True, False),
+    (4, 1, 4, 1, 256, 512, 1024, "f16", False, False),
+    (8, 1, 8, 1, 128, 256, 512, "f32", False, False),
+    (16, 1, 16, 1, 64, 128, 256, "f16", False, False),
+    (2, 4, 2, 4, 128, 256, 512, "f16", True, False),
+    (4, 2, 4, 2, 256, 512, 1024, "f32", True, False),
     (2, 4, 2, 4, 128, 256, 512, "f16", False, False),
+    (4, 2, 4, 2, 256, 512, 1024, "f32", False, False),
     (1, 1, 4, 1, 128, 256, 512, "f16", True, False),
+    (1, 1, 8, 1, 64, 128, 256, "f32", True, False),
+    (1, 1, 4, 1, 128, 256, 512, "f16", False, False),
+    (1, 1, 8, 1, 64, 128, 256, "f32", False, False),
+    (4, 1, 1, 1, 128, 256, 512, "f16", True, False),
     (8, 1, 1, 1, 64, 128, 256, "f32", True, False),
+    (4, 1, 1, 1, 128, 256, 512, "f16", False, False),
+    (8, 1, 1, 1, 64, 128, 256, "f32", False, False),
+    (1, 1, 1, 4, 128, 256, 512, "f16", True, False),
+    (1, 1, 1, 8, 64, 128, 256, "f32", True, False),
     (1, 1, 1, 4, 128, 256, 512, "f16", False, False),
+    (1, 1, 1, 8, 64, 128, 256, "f32", False, False),
     (1, 4, 1, 1, 128, 256, 512, "f16", True, False),
+    (1, 8, 1, 1, 64, 128, 256, "f32", True, False),
+    (1, 4, 1, 1, 128, 256, 512, "f16", False, False),
+    (1, 8, 1, 1, 64, 128, 256, "f32", False, False),
     (1, 1, 4, 4, 64, 128, 256, "f16", True, False),
-    (4, 4, 1, 1, 64, 128, 256, "f32", False, False),
+    (1, 1, 2, 8, 64, 128, 256, "f32", True, False),
+    (1, 1, 4, 4, 64, 128, 256, "f16", False, False),
+    (1, 1, 2, 8, 64, 128, 256, "f32", False, False),
+    (4, 4, 1, 1, 64, 128, 256, "f16", True, False),
+    (2, 8, 1, 1, 64, 128, 256, "f32", True, False),
+    (4, 4, 1, 1, 64, 128, 256, "f16", False, False),
+    (2, 8, 1, 1, 64, 128, 256, "f32", False, False),
     (1, 4, 4, 1, 64, 128, 256, "f16", True, False),
+    (1, 8, 8, 1, 64, 128, 256, "f32", True, False),
+    (1, 4, 4, 1, 64, 128, 256, "f16", False, False),
+    (1, 8, 8, 1, 64, 128, 256, "f32", False, False),
     (1, 1, 1, 1, 512, 1024, 2048, "f16", True, True),
     (1, 1, 1, 1, 333, 1259, 365, "f32", True, True),
     (1, 1, 1, 1, 256, 512, 1024, "f16", False, True),
+    (1, 1, 1, 1, 128, 256, 512, "f32", False, True),
     (4, 1, 4, 1, 256, 512, 1024, "f16", True, True),
+    (8, 1, 8, 1, 128, 256, 512, "f32", True, True),
+    (4, 1, 4, 1, 256, 512, 1024, "f16", False, True),
+    (8, 1, 8, 1, 128, 256, 512, "f32", False, True),
+    (2, 4, 2, 4, 128, 256, 512, "f16", True, True),
+    (4, 2, 4, 2, 256, 512, 1024, "f32", True, True),
+    (1, 1, 4, 1, 128, 256, 512, "f16", True, True),
+    (4, 1, 1, 1, 128, 256, 512, "f32", True, True),
+    (1, 1, 1, 4, 128, 256, 512, "f16", True, True),
+    (1, 4, 1, 1, 64, 128, 256, "f32", True, True),
     (1, 1, 4, 4, 64, 128, 256, "f16", True, True),
+    (4, 4, 1, 1, 64, 128, 256, "f32", True, True),
+    (1, 4, 4, 1, 64, 128, 256, "f16", True, True),
     # the token step's decode shapes
     (1, 1, 1, 1, 1, 4096, 11008, "f16", True, False),
     (1, 1, 1, 1, 1, 288, 768, "f16", True, True),

@@ -238,13 +238,15 @@ void timing_begin(vkllm_context *ctx, vkllm_pipeline *p)
 void timing_end(vkllm_context *ctx, vkllm_pipeline *p)
 {
     vkllm_gpu_device *dev = ctx->device;
+    vkllm_pipeline *node = dev->timing_node; // applies to this launch only
+    dev->timing_node = nullptr;
     if (!dev->timing || !p->ev_begin)
         return;
     hipEvent_t e = pooled_event(dev);
     if (!e)
         return;
     (void)hipEventRecord(e, dev->stream);
-    dev->timing_pending.push_back({p, (hipEvent_t)p->ev_begin, e});
+    dev->timing_pending.push_back({p, (hipEvent_t)p->ev_begin, e, node});
     p->ev_begin = nullptr;
     p->pending = 1;
     // bound the number of events in flight; the flush waits for the oldest launches only
@@ -264,9 +266,17 @@ hipError_t timing_flush(vkllm_context *ctx)
             e = hipEventElapsedTime(&ms, r.begin, r.end);
         if (e == hipSuccess)
         {
-            r.pipeline->last_ns = (uint64_t)((double)ms * 1e6);
-            r.pipeline->total_ns += r.pipeline->last_ns;
+            const uint64_t ns = (uint64_t)((double)ms * 1e6);
+            r.pipeline->last_ns = ns;
+            r.pipeline->total_ns += ns;
             r.pipeline->launches += 1;
+            if (r.node)
+            {
+                // a node's last_ns is the sum over the launches of the step that computed it
+                r.node->last_ns += ns;
+                r.node->total_ns += ns;
+                r.node->launches += 1;
+            }
         }
         else if (rc == hipSuccess)
             rc = e;

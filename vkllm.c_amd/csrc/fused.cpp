@@ -15,6 +15,9 @@
 #include <cstdlib>
 #include <cstring>
 #include <ctime>
+#include <string>
+#include <unordered_map>
+#include <vector>
 
 #include "model_priv.h"
 
@@ -73,10 +76,69 @@ struct FusedState
     // the positions bound of the short-cache launches being enqueued (the current variant's)
     uint32_t small_kv_max = 0;
     int last_exec = -1;
+    // timing mode: one record per graph node a fused launch computes (per layer, then the step's own nodes), named
+    // as the node; after a timed step the graph's nodes point at the records that received launches
+    std::vector<vkllm_pipeline> node_pipes;
+    std::vector<std::string> node_names;
+    std::unordered_map<std::string, int> node_index;
     // VKLLM_TRACE_HOST=1: host time of single-token steps spent enqueueing and waiting, printed at release
     bool trace = false;
     uint64_t trace_steps = 0, trace_enqueue_ns = 0, trace_wait_ns = 0;
 };
+
+// Graph nodes (src/models/vkllm_llama2_layers.c:98-354, src/models/vkllm_models_llama2.c:488-602) that the fused
+// launches are charged to in timing mode: the node a launch computes, or the first of the nodes it computes.
+enum NodeSlot
+{
+    NS_ATTN_NORM = 0, // block.l.attn.norm: the prompt step's RMSNorm pass
+    NS_Q,             // block.l.attn.Q: the QKV product (with RMSNorm, RoPE and the K/V append where fused)
+    NS_RQ,            // block.l.attn.RQ: the separate RoPE + K/V append
+    NS_RK,            // block.l.attn.RK: the prompt step's RoPE angle table (layer 0)
+    NS_SCORES,        // block.l.attn.scores: attention (scores, softmax, P.V) in one launch, or its scores part
+    NS_ATTN,          // block.l.attn: the P.V part of a two-launch attention
+    NS_WO,            // block.l.attn.final_output: Wo + residual
+    NS_FFN_NORM,      // block.l.ffn.norm
+    NS_UP,            // block.l.ffn.up: the up/gate product with SwiGLU
+    NS_MUL,           // block.l.ffn.mul: the separate SwiGLU
+    NS_DOWN,          // block.l.ffn.down: Wd + residual
+    NS_PER_LAYER,
+    // the step's own nodes, after the layers
+    NS_EMBEDDED = 0,
+    NS_OUTPUT_NORM,
+    NS_LOGITS,
+    NS_OUTPUT,
+    NS_GLOBAL
+};
+
+static void make_node_records(FusedState *fs, uint32_t L)
+{
+    static const char *per_layer[NS_PER_LAYER] = {"attn.norm", "attn.Q",  "attn.RQ",  "attn.RK",  "attn.scores", "attn",
+                                                  "attn.final_output", "ffn.norm", "ffn.up", "ffn.mul", "ffn.down"};
+    static const char *global[NS_GLOBAL] = {"embedded", "output_norm", "logits", "output"};
+    const size_t n = (size_t)L * NS_PER_LAYER + NS_GLOBAL;
+    fs->node_names.reserve(n);
+    for (uint32_t l = 0; l < L; ++l)
+        for (int k = 0; k < NS_PER_LAYER; ++k)
+            fs->node_names.push_back("block." + std::to_string(l) + "." + per_layer[k]);
+    for (int k = 0; k < NS_GLOBAL; ++k)
+        fs->node_names.push_back(global[k]);
+    fs->node_pipes.assign(n, vkllm_pipeline{});
+    for (size_t i = 0; i < n; ++i)
+    {
+        fs->node_pipes[i].name = fs->node_names[i].c_str();
+        fs->node_pipes[i].kernel_id = -1;
+        fs->node_index.emplace(fs->node_names[i], (int)i);
+    }
+}
+
+// the next timed launch is charged to node `slot` of layer l (or, with l == UINT32_MAX, the step's node `slot`)
+static void charge(vkllm_context *ctx, FusedState *fs, int slot, uint32_t l = UINT32_MAX)
+{
+    if (!ctx->device->timing || fs->node_pipes.empty())
+        return;
+    const size_t L = (fs->node_pipes.size() - NS_GLOBAL) / NS_PER_LAYER;
+    ctx->device->timing_node = &fs->node_pipes[l == UINT32_MAX ? L * NS_PER_LAYER + slot : (size_t)l * NS_PER_LAYER + slot];
+}
 
 // split-K workspace of the prefill GEMMs: 64 MB of fp32 partial tiles (4 splits of a 128-row QKV product at
 // dim 5120 need 31 MB)
@@ -219,6 +281,7 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         HIP_TRY(hipMalloc(&fs->att_long_sync, H * vk::kAttnLongStride * sizeof(uint32_t)));
         HIP_TRY(hipMemset(fs->att_long_sync, 0, H * vk::kAttnLongStride * sizeof(uint32_t)));
         HIP_TRY(hipMalloc(&fs->gemm_work, kGemmWorkElems * sizeof(float)));
+        make_node_records(fs, mp->L);
     }
     FusedState *fs = mp->fs;
     if (S <= fs->cap_S)
@@ -370,7 +433,43 @@ static hipError_t launch_decode_kernel(vkllm_context *ctx, ModelPriv *mp, Kernel
     }
 }
 
-#define DTRY(_ctx, _mp, _kid, _l) KTRY(_ctx, _kid, launch_decode_kernel((_ctx), (_mp), (_kid), (_l)))
+// the node a single-token step's launch of family kid is charged to
+static void charge_decode(vkllm_context *ctx, FusedState *fs, KernelId kid, uint32_t l)
+{
+    switch (kid)
+    {
+    case KID_F_EMBED:
+        return charge(ctx, fs, NS_EMBEDDED);
+    case KID_F_QKV:
+        return charge(ctx, fs, NS_Q, l);
+    case KID_F_ATTN_SMALL:
+    case KID_F_ATTN_LONG:
+    case KID_F_ATTN_SCORES:
+    case KID_F_ATTN_O:
+        return charge(ctx, fs, NS_SCORES, l);
+    case KID_F_ATTN_PV:
+        return charge(ctx, fs, NS_ATTN, l);
+    case KID_F_O_RESID:
+        return charge(ctx, fs, NS_WO, l);
+    case KID_F_GATEUP:
+        return charge(ctx, fs, NS_UP, l);
+    case KID_F_DOWN_RESID:
+        return charge(ctx, fs, NS_DOWN, l);
+    case KID_F_LOGITS:
+        return charge(ctx, fs, NS_LOGITS);
+    case KID_F_ARGMAX:
+        return charge(ctx, fs, NS_OUTPUT);
+    default:
+        return;
+    }
+}
+
+#define DTRY(_ctx, _mp, _kid, _l)                                                                                   \
+    do                                                                                                              \
+    {                                                                                                               \
+        charge_decode((_ctx), (_mp)->fs, (_kid), (_l));                                                             \
+        KTRY(_ctx, _kid, launch_decode_kernel((_ctx), (_mp), (_kid), (_l)));                                        \
+    } while (0)
 
 // the attention variant of a single-token step at cache length kv: the short-cache bucket b < kSmallBuckets, or
 // kSmallBuckets for the long-cache path
@@ -396,6 +495,7 @@ static vkllm_err_t enqueue_decode(vkllm_context *ctx, ModelPriv *mp, uint32_t va
         bool fused_o = false;
         if (small_attn && mp->fs->attn_o)
         {
+            charge_decode(ctx, mp->fs, KID_F_ATTN_O, l);
             const hipError_t e = timed(ctx, pipeline_of(ctx, KID_F_ATTN_O),
                                        [&]() { return launch_decode_kernel(ctx, mp, KID_F_ATTN_O, l); });
             if (e == hipSuccess)
@@ -410,6 +510,7 @@ static vkllm_err_t enqueue_decode(vkllm_context *ctx, ModelPriv *mp, uint32_t va
             bool long_done = false;
             if (!small_attn && mp->fs->attn_long)
             {
+                charge_decode(ctx, mp->fs, KID_F_ATTN_LONG, l);
                 const hipError_t e = timed(ctx, pipeline_of(ctx, KID_F_ATTN_LONG),
                                            [&]() { return launch_decode_kernel(ctx, mp, KID_F_ATTN_LONG, l); });
                 if (e == hipSuccess)
@@ -443,14 +544,19 @@ static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S
     const int cu = ctx->device->cu_count;
     const uint32_t D = mp->D, F = mp->F, V = mp->V, hd = mp->hd;
     const float scale = 1.0f / sqrtf((float)hd);
+    charge(ctx, fs, NS_EMBEDDED);
     KTRY(ctx, KID_F_EMBED, vk::launch_embed_rows(st, fs->toks, S, mp->embd, fs->h, V, D, mp->pad_id));
     // RoPE in the QKV product's epilogue where the shape allows it (angles computed once for all layers);
     // otherwise the product is stored and a separate kernel rotates and appends
     const bool rope_epi = fs->rope_epi && D % 64 == 0 && hd >= 32 && (hd & (hd - 1)) == 0;
     if (rope_epi)
+    {
+        charge(ctx, fs, NS_RK, 0);
         KTRY(ctx, KID_F_ROPE_KV, vk::launch_rope_table(st, fs->rope_cs, fs->freqs, offset, S, hd));
+    }
     // every residual product also leaves the next RMSNorm of the residual stream in xn (in the split-K reduce when
     // K is split, else as a separate pass)
+    charge(ctx, fs, NS_ATTN_NORM, 0);
     KTRY(ctx, KID_F_RMSNORM, vk::launch_rmsnorm_rows(st, fs->h, mp->layers[0].attn_norm, fs->xn, S, D, mp->eps));
     for (uint32_t l = 0; l < mp->L; ++l)
     {
@@ -458,22 +564,31 @@ static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S
         if (rope_epi)
         {
             const vk::GemmRope rope{fs->q, ly.kc, ly.vc, fs->rope_cs, offset, D, hd, mp->ctx};
+            charge(ctx, fs, NS_Q, l);
             KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_QKV_ROPE, fs->xn, ly.wqkv, fs->qkv, S, 3 * D, D, 3 * D, 0, cu, fs->gemm_work, kGemmWorkElems, &rope));
         }
         else
         {
+            charge(ctx, fs, NS_Q, l);
             KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_PLAIN, fs->xn, ly.wqkv, fs->qkv, S, 3 * D, D, 3 * D, 0, cu, fs->gemm_work, kGemmWorkElems));
+            charge(ctx, fs, NS_RQ, l);
             KTRY(ctx, KID_F_ROPE_KV,
                  vk::launch_rope_kv(st, fs->qkv, fs->q, ly.kc, ly.vc, fs->freqs, offset, S, D, hd, mp->ctx));
         }
+        charge(ctx, fs, NS_SCORES, l);
         KTRY(ctx, KID_F_ATTN_PREFILL,
              vk::launch_attn_prefill(st, fs->q, ly.kc, ly.vc, fs->attn, offset, S, mp->H, hd, mp->ctx, scale));
         const vk::GemmNorm ffn_norm{ly.ffn_norm, fs->xn, mp->eps};
+        charge(ctx, fs, NS_WO, l);
         KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_RESID, fs->attn, ly.wo, fs->h, S, D, D, D, 0, cu, fs->gemm_work, kGemmWorkElems, nullptr, fs->norm_epi ? &ffn_norm : nullptr));
         if (!fs->norm_epi)
+        {
+            charge(ctx, fs, NS_FFN_NORM, l);
             KTRY(ctx, KID_F_RMSNORM, vk::launch_rmsnorm_rows(st, fs->h, ly.ffn_norm, fs->xn, S, D, mp->eps));
+        }
         // SwiGLU in the product's epilogue where the shape allows it (gate and up rows read as interleaved blocks);
         // otherwise up and SiLU(gate) are stored side by side and multiplied by a separate kernel
+        charge(ctx, fs, NS_UP, l);
         if (D % 64 == 0 && F % 32 == 0)
             KTRY(ctx, KID_F_GEMM,
                  vk::launch_gemm(st, vk::GEMM_SWIGLU, fs->xn, ly.wug, fs->act, S, 2 * F, D, F, F, cu, fs->gemm_work, kGemmWorkElems));
@@ -481,14 +596,24 @@ static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S
         {
             KTRY(ctx, KID_F_GEMM,
                  vk::launch_gemm(st, vk::GEMM_SILU_HI, fs->xn, ly.wug, fs->ug, S, 2 * F, D, 2 * F, F, cu, fs->gemm_work, kGemmWorkElems));
+            charge(ctx, fs, NS_MUL, l);
             KTRY(ctx, KID_F_SWIGLU, vk::launch_swiglu(st, fs->ug, fs->act, S, F));
         }
         const vk::GemmNorm next_norm{l + 1 < mp->L ? mp->layers[l + 1].attn_norm : mp->out_norm, fs->xn, mp->eps};
+        charge(ctx, fs, NS_DOWN, l);
         KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_RESID, fs->act, ly.wd, fs->h, S, D, F, D, 0, cu, fs->gemm_work, kGemmWorkElems, nullptr, fs->norm_epi ? &next_norm : nullptr));
         if (!fs->norm_epi)
+        {
+            if (l + 1 < mp->L)
+                charge(ctx, fs, NS_ATTN_NORM, l + 1);
+            else
+                charge(ctx, fs, NS_OUTPUT_NORM);
             KTRY(ctx, KID_F_RMSNORM, vk::launch_rmsnorm_rows(st, fs->h, next_norm.w, fs->xn, S, D, mp->eps));
+        }
     }
+    charge(ctx, fs, NS_LOGITS);
     KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_PLAIN, fs->xn, mp->out_w, fs->logits, S, V, D, V, 0, cu, fs->gemm_work, kGemmWorkElems));
+    charge(ctx, fs, NS_OUTPUT);
     KTRY(ctx, KID_F_ARGMAX, vk::launch_argmax_rows(st, fs->logits, fs->ids, S, V));
     return VKLLM_ERR_OK;
 }
@@ -538,12 +663,42 @@ static vkllm_err_t launch_decode_step(vkllm_context *ctx, ModelPriv *mp, uint32_
     return VKLLM_ERR_OK;
 }
 
+// Timing mode: the step's node records start from zero (pending launches of earlier work are read first)
+static vkllm_err_t reset_node_costs(vkllm_context *ctx, FusedState *fs)
+{
+    if (!ctx->device->timing)
+        return VKLLM_ERR_OK;
+    HIP_TRY(timing_flush(ctx));
+    for (vkllm_pipeline &r : fs->node_pipes)
+        r.last_ns = 0;
+    return VKLLM_ERR_OK;
+}
+
+// Timing mode, after the step: each graph node whose record received launches points at it, so
+// vkllm_pipeline_query_exec_time(node->pipeline) gives the node's share of the step, as the reference's per-node
+// timestamps do (tests/vkllm_test_infer_gguf.c:205-225). The records sum to the step's kernel time.
+static vkllm_err_t attach_node_costs(vkllm_context *ctx, FusedState *fs, vkllm_graph *graph)
+{
+    if (!ctx->device->timing)
+        return VKLLM_ERR_OK;
+    HIP_TRY(timing_flush(ctx));
+    for (size_t i = 0; i < graph->nodes->used_n; ++i)
+    {
+        vkllm_tensor *t = graph->nodes->data[i];
+        auto it = fs->node_index.find(t->name);
+        if (it != fs->node_index.end() && fs->node_pipes[it->second].last_ns > 0)
+            t->pipeline = &fs->node_pipes[it->second];
+    }
+    return VKLLM_ERR_OK;
+}
+
 vkllm_err_t fused_plan_run(vkllm_context *ctx, vkllm_graph *graph)
 {
     auto *p = (FusedPlan *)graph->plan;
     ModelPriv *mp = model_priv(p->model);
     _CHECK(fused_plan_init(ctx, graph));
     FusedState *fs = mp->fs;
+    _CHECK(reset_node_costs(ctx, fs));
     hipStream_t st = ctx->device->stream;
     const uint32_t S = p->S;
     // the step's ids are in the mapped input tensor's host mirror (written by vkllm_commands_upload)
@@ -607,7 +762,7 @@ vkllm_err_t fused_plan_run(vkllm_context *ctx, vkllm_graph *graph)
         memcpy(out->data.host, fs->io_h, (size_t)S * 4);
         out->data.host_current = true;
         out->data.valid = false;
-        return VKLLM_ERR_OK;
+        return attach_node_costs(ctx, fs, graph);
     }
     void *out_dev = tensor_dev(ctx, out);
     if (!out_dev)
@@ -615,7 +770,7 @@ vkllm_err_t fused_plan_run(vkllm_context *ctx, vkllm_graph *graph)
     HIP_TRY(hipMemcpyAsync(out_dev, fs->ids, (size_t)S * 4, hipMemcpyDeviceToDevice, st));
     HIP_TRY(hipStreamSynchronize(st));
     out->data.valid = true;
-    return VKLLM_ERR_OK;
+    return attach_node_costs(ctx, fs, graph);
 }
 
 // ---- extension: fused-step internals for tests and measurement ----

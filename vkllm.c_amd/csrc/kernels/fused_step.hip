@@ -329,6 +329,12 @@ template <int EPI, int R> __device__ __forceinline__ void gemv_epilogue(const Ge
     }
 }
 
+// the epilogues whose input is the RMSNorm of the residual stream (all but the residual products)
+constexpr bool gemv_normalises(int epi)
+{
+    return epi != EPI_RESID;
+}
+
 template <int EPI, int R, int NV> __global__ __launch_bounds__(256) void gemv_fast_kernel(GemvArgs a, uint32_t units)
 {
     extern __shared__ u32x4 xs[];
@@ -336,20 +342,21 @@ template <int EPI, int R, int NV> __global__ __launch_bounds__(256) void gemv_fa
     constexpr int XV = (NV * 64 + 255) / 256; // input vectors per thread
     const uint32_t tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
     const uint32_t nvec = a.K / 8;
-    const bool norm = a.norm_w != nullptr;
+    // the residual products (Wo, Wd) take their input as is; the others normalise it (the launcher checks norm_w)
+    constexpr bool norm = gemv_normalises(EPI);
 
     // 1. input share (and RMSNorm weights)
     // Loads are unconditional at clamped addresses (a guarded load compiles to a branch and a full wait per load);
     // lanes past the end read a valid duplicate that is masked out below.
     u32x4 xr[XV];
-    float4 nw[XV][2];
+    float4 nw[norm ? XV : 1][2];
     const float4 *nwp = (const float4 *)(norm ? a.norm_w : (const float *)a.x);
 #pragma unroll
     for (int i = 0; i < XV; ++i)
     {
         const uint32_t vi = min(tid + 256 * i, nvec - 1);
         xr[i] = ((const u32x4 *)a.x)[vi];
-        if (norm)
+        if constexpr (norm)
         {
             nw[i][0] = nwp[2 * vi];
             nw[i][1] = nwp[2 * vi + 1];
@@ -399,7 +406,7 @@ template <int EPI, int R, int NV> __global__ __launch_bounds__(256) void gemv_fa
     load_unit(u);
 
     // 3. prologue
-    if (norm)
+    if constexpr (norm)
     {
         float ss = 0.f;
 #pragma unroll
@@ -490,7 +497,7 @@ static uint32_t gemv_units(int epi, const GemvArgs &a, int R)
 template <int EPI, int R, int NV> static hipError_t launch_fast(hipStream_t st, const GemvArgs &a, int cu_count)
 {
     const uint32_t units = gemv_units(EPI, a, R);
-    if (units == 0)
+    if (units == 0 || (a.norm_w != nullptr) != gemv_normalises(EPI))
         return hipErrorInvalidValue;
     // resident workgroups per CU at this kernel's register use and this K's LDS, cached for the last K seen
     static size_t cached_lds = 0;

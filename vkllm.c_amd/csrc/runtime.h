@@ -86,7 +86,10 @@ struct vkllm_gpu_device
     {
         vkllm_pipeline *pipeline;
         hipEvent_t begin, end;
+        vkllm_pipeline *node; // optional: a graph node's record, whose last_ns also receives the launch's duration
     };
+    // the node record the next timed launch adds its duration to (set by the fused executor, taken by timing_end)
+    vkllm_pipeline *timing_node = nullptr;
     std::vector<TimingRec> timing_pending;
     std::vector<hipEvent_t> event_pool;
 };
