@@ -31,7 +31,7 @@ struct FusedPlan
 
 // Short-cache decode steps are captured per bucket of kSmallBucket cache positions: a bucket's launches bound their
 // LDS and the keys and V rows they request before the position is known by the bucket's end.
-constexpr uint32_t kSmallBucket = 128, kSmallBuckets = 12;
+constexpr uint32_t kSmallBucket = 64, kSmallBuckets = 24;
 
 struct FusedState
 {
