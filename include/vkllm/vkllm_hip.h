@@ -97,6 +97,17 @@ extern vkllm_err_t vkllm_hip_gemm(struct vkllm_context *context, int epi, const 
                                   uint16_t *C, uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split,
                                   float *work, uint64_t work_elems);
 
+/* The short-prompt product of the fused step (prompts of at most 128 tokens), with vkllm_hip_gemm's arguments and
+ * epilogues 0 (C = fp16(acc), ldc >= N), 2 (C = fp16(C + fp16(acc)), ldc == N, N % 32 == 0) and 3 (the SwiGLU of
+ * B = [Wu; Wg], N = 2F, F % 16 == 0, ldc >= F); M <= 128, K % 16 == 0, A and B 16-byte aligned, C 8-byte aligned,
+ * ldc % 4 == 0. It copies B into the fragment-tiled layout the fused step keeps for its weights and A into
+ * fragment order (allocating both), then streams the weights through the matrix cores; `splits` (at most 8; 0 for
+ * the fused step's choice) sets the K ranges of epilogue 2. Returns when C is written. There is no counterpart in
+ * the reference: this exposes the kernel behind the fused step's short-prompt matmul nodes for checks and timing. */
+extern vkllm_err_t vkllm_hip_gemm_streamed(struct vkllm_context *context, int epi, const uint16_t *A,
+                                           const uint16_t *B, uint16_t *C, uint32_t M, uint32_t N, uint32_t K,
+                                           uint32_t ldc, uint32_t splits);
+
 /* vkllm_hip_gemm for callers that cannot allocate device memory (code under stream capture, serving loops that
  * forbid hipMalloc). It has no counterpart in the reference. The split-K partial tiles go to a fixed scratch array
  * of the library (8M floats, 32 MiB, held by every GPU the library runs on until the process ends) instead of a

@@ -220,6 +220,8 @@ def test_qkv_rope_epilogue_matches_separate_kernel(ctx, vk, monkeypatch, prompt_
     reading the appended cache; identical ids and logits."""
     shape = dict(n_layer=2, dim=4096, n_head=32, ffn=11008, vocab=32000, ctx=1100)
     prompt = vk.prompt_tokens(9, prompt_len, shape["vocab"])
+    # both arms on the tile GEMMs (the streamed short-prompt products need the epilogue and sum in another order)
+    monkeypatch.setenv("VKLLM_PREFILL_TILED", "0")
     monkeypatch.setenv("VKLLM_ROPE_EPI", "1")
     ids_a, logits_a = _device_loop(ctx, vk, shape, 7, prompt, 4)
     monkeypatch.setenv("VKLLM_ROPE_EPI", "0")
@@ -235,6 +237,8 @@ def test_norm_in_split_k_reduce_matches_separate_pass(ctx, vk, monkeypatch, prom
     logits."""
     shape = dict(n_layer=2, dim=4096, n_head=32, ffn=11008, vocab=32000, ctx=160)
     prompt = vk.prompt_tokens(10, prompt_len, shape["vocab"])
+    # both arms on the tile GEMMs (the streamed short-prompt products need the fused norm and sum in another order)
+    monkeypatch.setenv("VKLLM_PREFILL_TILED", "0")
     monkeypatch.setenv("VKLLM_NORM_EPI", "1")
     ids_a, logits_a = _device_loop(ctx, vk, shape, 7, prompt, 4)
     monkeypatch.setenv("VKLLM_NORM_EPI", "0")

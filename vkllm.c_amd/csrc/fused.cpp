@@ -51,6 +51,17 @@ struct FusedState
     uint32_t *attn_sync = nullptr; // counters and flags of the attention + projection launch, zero between launches
     uint32_t *att_long_sync = nullptr; // per-head counters of the one-kernel long-cache attention, zero between launches
     float *gemm_work = nullptr;    // split-K partial tiles of short-prompt prefill GEMMs
+    // prompt steps of at most 128 tokens (VKLLM_PREFILL_TILED=0: off): fragment-tiled copies of the QKV, output,
+    // gate/up and vocabulary matrices (one slab), streamed by launch_stream_gemm, and the fragment-ordered
+    // activations it reads ([128, D] each: the normalised rows and the attention output)
+    bool stream_ok = false;
+    void *tile_slab = nullptr;
+    struct Tiles
+    {
+        uint16_t *wqkv, *wo, *wug;
+    };
+    std::vector<Tiles> tiles;
+    uint16_t *out_t = nullptr, *xn_t = nullptr, *attn_t = nullptr;
     uint32_t att_cmax = 0, att_chunk = 0;
     uint32_t attn_max_groups = 8; // dim slices per head of the short-cache attention, at most (VKLLM_ATTN_GROUPS)
     // decode attention in one kernel up to this many positions, in two kernels beyond (VKLLM_ATTN_SMALL_MAX)
@@ -211,7 +222,7 @@ void fused_model_release(vkllm_context *ctx, vkllm_models_llama2 *model)
     if (fs->freqs)
         (void)hipFree(fs->freqs);
     void *att[] = {fs->att_scores, fs->att_stats, fs->att_part, fs->att_count, fs->attn_sync, fs->att_long_sync,
-                   fs->gemm_work};
+                   fs->gemm_work,  fs->tile_slab, fs->xn_t,      fs->attn_t};
     for (void *b : att)
         if (b)
             (void)hipFree(b);
@@ -223,6 +234,60 @@ void fused_model_release(vkllm_context *ctx, vkllm_models_llama2 *model)
         (void)hipHostFree(fs->dio);
     delete fs;
     mp->fs = nullptr;
+}
+
+// The fragment-tiled weight copies of the short-prompt products, made once from the slab. Shapes the streamed
+// products and their producers cannot take, or too little free memory, leave stream_ok false (those steps then run
+// on the row-major slab).
+static vkllm_err_t build_stream_tiles(vkllm_context *ctx, ModelPriv *mp)
+{
+    FusedState *fs = mp->fs;
+    const char *e = getenv("VKLLM_PREFILL_TILED");
+    if (e && *e == '0')
+        return VKLLM_ERR_OK;
+    const uint32_t D = mp->D, F = mp->F, V = mp->V, hd = mp->hd;
+    // the QKV product's RoPE epilogue, the MFMA attention's fragment-ordered output, the interleaved gate/up rows
+    if (D % 64 != 0 || F % 16 != 0 || hd < 32 || (hd & (hd - 1)) != 0 || !vk::attn_prefill_mfma_ok(hd))
+        return VKLLM_ERR_OK;
+    const size_t per_layer = vk::stream_tiled_elems(3 * D, D, 0) + vk::stream_tiled_elems(D, D, 0) +
+                             vk::stream_tiled_elems(2 * F, D, F);
+    const size_t total = per_layer * mp->L + vk::stream_tiled_elems(V, D, 0);
+    size_t free_b = 0, total_b = 0;
+    HIP_TRY(hipMemGetInfo(&free_b, &total_b));
+    if (total * 2 + (size_t)2 * 128 * D * 2 > free_b / 2)
+    {
+        log_error("short-prompt tiled weights need %.1f GB; %.1f GB free: prompt steps run on the row-major weights",
+                  total * 2 / 1e9, free_b / 1e9);
+        return VKLLM_ERR_OK;
+    }
+    hipStream_t st = ctx->device->stream;
+    HIP_TRY(hipMalloc(&fs->tile_slab, total * 2));
+    HIP_TRY(hipMalloc(&fs->xn_t, (size_t)128 * D * 2));
+    HIP_TRY(hipMalloc(&fs->attn_t, (size_t)128 * D * 2));
+    // rows past a step's tokens are read (their outputs are dropped): keep them finite
+    HIP_TRY(hipMemsetAsync(fs->xn_t, 0, (size_t)128 * D * 2, st));
+    HIP_TRY(hipMemsetAsync(fs->attn_t, 0, (size_t)128 * D * 2, st));
+    uint16_t *p = (uint16_t *)fs->tile_slab;
+    fs->tiles.resize(mp->L);
+    for (uint32_t l = 0; l < mp->L; ++l)
+    {
+        const ModelPriv::Layer &ly = mp->layers[l];
+        FusedState::Tiles &t = fs->tiles[l];
+        t.wqkv = p;
+        HIP_TRY(vk::launch_tile_weights(st, ly.wqkv, t.wqkv, 3 * D, D, 0));
+        p += vk::stream_tiled_elems(3 * D, D, 0);
+        t.wo = p;
+        HIP_TRY(vk::launch_tile_weights(st, ly.wo, t.wo, D, D, 0));
+        p += vk::stream_tiled_elems(D, D, 0);
+        t.wug = p;
+        HIP_TRY(vk::launch_tile_weights(st, ly.wug, t.wug, 2 * F, D, F));
+        p += vk::stream_tiled_elems(2 * F, D, F);
+    }
+    fs->out_t = p;
+    HIP_TRY(vk::launch_tile_weights(st, mp->out_w, fs->out_t, V, D, 0));
+    HIP_TRY(hipStreamSynchronize(st));
+    fs->stream_ok = true;
+    return VKLLM_ERR_OK;
 }
 
 static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
@@ -282,6 +347,7 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         HIP_TRY(hipMemset(fs->att_long_sync, 0, H * vk::kAttnLongStride * sizeof(uint32_t)));
         HIP_TRY(hipMalloc(&fs->gemm_work, kGemmWorkElems * sizeof(float)));
         make_node_records(fs, mp->L);
+        _CHECK(build_stream_tiles(ctx, mp));
     }
     FusedState *fs = mp->fs;
     if (S <= fs->cap_S)
@@ -537,6 +603,19 @@ static vkllm_err_t enqueue_decode(vkllm_context *ctx, ModelPriv *mp, uint32_t va
     return VKLLM_ERR_OK;
 }
 
+// A short-prompt product streamed from its tiled weights; a STREAM_PARTIAL product then goes through the split-K
+// reduce with `reduce_epi` (GEMM_QKV_ROPE with `rope`, or GEMM_RESID into C with `norm`).
+static hipError_t stream_product(hipStream_t st, FusedState *fs, int epi, const uint16_t *X, const uint16_t *Wt,
+                                 uint16_t *C, uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, int reduce_epi = -1,
+                                 const vk::GemmRope *rope = nullptr, const vk::GemmNorm *norm = nullptr)
+{
+    uint32_t splits = 0;
+    hipError_t e = vk::launch_stream_gemm(st, epi, X, Wt, C, fs->gemm_work, kGemmWorkElems, M, N, K, ldc, &splits);
+    if (e != hipSuccess || epi != vk::STREAM_PARTIAL)
+        return e;
+    return vk::launch_gemm_reduce(st, reduce_epi, fs->gemm_work, C, M, N, splits, rope, norm);
+}
+
 static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S, uint32_t offset)
 {
     FusedState *fs = mp->fs;
@@ -556,12 +635,23 @@ static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S
     }
     // every residual product also leaves the next RMSNorm of the residual stream in xn (in the split-K reduce when
     // K is split, else as a separate pass)
+    // prompts of at most 128 tokens: the QKV, output, gate/up and vocabulary products stream their tiled weights,
+    // reading fragment-ordered activations (the normalised rows in xn_t, the attention output in attn_t)
+    const bool streamed = fs->stream_ok && S <= 128 && rope_epi && fs->norm_epi;
+    uint16_t *xn = streamed ? fs->xn_t : fs->xn;
+    uint16_t *attn = streamed ? fs->attn_t : fs->attn;
     charge(ctx, fs, NS_ATTN_NORM, 0);
-    KTRY(ctx, KID_F_RMSNORM, vk::launch_rmsnorm_rows(st, fs->h, mp->layers[0].attn_norm, fs->xn, S, D, mp->eps));
+    KTRY(ctx, KID_F_RMSNORM, vk::launch_rmsnorm_rows(st, fs->h, mp->layers[0].attn_norm, xn, S, D, mp->eps, streamed));
     for (uint32_t l = 0; l < mp->L; ++l)
     {
         const ModelPriv::Layer &ly = mp->layers[l];
-        if (rope_epi)
+        if (streamed)
+        {
+            const vk::GemmRope rope{fs->q, ly.kc, ly.vc, fs->rope_cs, offset, D, hd, mp->ctx};
+            charge(ctx, fs, NS_Q, l);
+            KTRY(ctx, KID_F_GEMM, stream_product(st, fs, vk::STREAM_PARTIAL, xn, fs->tiles[l].wqkv, fs->qkv, S, 3 * D, D, 3 * D, vk::GEMM_QKV_ROPE, &rope));
+        }
+        else if (rope_epi)
         {
             const vk::GemmRope rope{fs->q, ly.kc, ly.vc, fs->rope_cs, offset, D, hd, mp->ctx};
             charge(ctx, fs, NS_Q, l);
@@ -577,10 +667,13 @@ static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S
         }
         charge(ctx, fs, NS_SCORES, l);
         KTRY(ctx, KID_F_ATTN_PREFILL,
-             vk::launch_attn_prefill(st, fs->q, ly.kc, ly.vc, fs->attn, offset, S, mp->H, hd, mp->ctx, scale));
-        const vk::GemmNorm ffn_norm{ly.ffn_norm, fs->xn, mp->eps};
+             vk::launch_attn_prefill(st, fs->q, ly.kc, ly.vc, attn, offset, S, mp->H, hd, mp->ctx, scale, streamed));
+        const vk::GemmNorm ffn_norm{ly.ffn_norm, xn, mp->eps, streamed};
         charge(ctx, fs, NS_WO, l);
-        KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_RESID, fs->attn, ly.wo, fs->h, S, D, D, D, 0, cu, fs->gemm_work, kGemmWorkElems, nullptr, fs->norm_epi ? &ffn_norm : nullptr));
+        if (streamed)
+            KTRY(ctx, KID_F_GEMM, stream_product(st, fs, vk::STREAM_PARTIAL, attn, fs->tiles[l].wo, fs->h, S, D, D, D, vk::GEMM_RESID, nullptr, &ffn_norm));
+        else
+            KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_RESID, fs->attn, ly.wo, fs->h, S, D, D, D, 0, cu, fs->gemm_work, kGemmWorkElems, nullptr, fs->norm_epi ? &ffn_norm : nullptr));
         if (!fs->norm_epi)
         {
             charge(ctx, fs, NS_FFN_NORM, l);
@@ -589,7 +682,9 @@ static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S
         // SwiGLU in the product's epilogue where the shape allows it (gate and up rows read as interleaved blocks);
         // otherwise up and SiLU(gate) are stored side by side and multiplied by a separate kernel
         charge(ctx, fs, NS_UP, l);
-        if (D % 64 == 0 && F % 32 == 0)
+        if (streamed)
+            KTRY(ctx, KID_F_GEMM, stream_product(st, fs, vk::STREAM_SWIGLU, xn, fs->tiles[l].wug, fs->act, S, 2 * F, D, F));
+        else if (D % 64 == 0 && F % 32 == 0)
             KTRY(ctx, KID_F_GEMM,
                  vk::launch_gemm(st, vk::GEMM_SWIGLU, fs->xn, ly.wug, fs->act, S, 2 * F, D, F, F, cu, fs->gemm_work, kGemmWorkElems));
         else
@@ -599,7 +694,7 @@ static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S
             charge(ctx, fs, NS_MUL, l);
             KTRY(ctx, KID_F_SWIGLU, vk::launch_swiglu(st, fs->ug, fs->act, S, F));
         }
-        const vk::GemmNorm next_norm{l + 1 < mp->L ? mp->layers[l + 1].attn_norm : mp->out_norm, fs->xn, mp->eps};
+        const vk::GemmNorm next_norm{l + 1 < mp->L ? mp->layers[l + 1].attn_norm : mp->out_norm, xn, mp->eps, streamed};
         charge(ctx, fs, NS_DOWN, l);
         KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_RESID, fs->act, ly.wd, fs->h, S, D, F, D, 0, cu, fs->gemm_work, kGemmWorkElems, nullptr, fs->norm_epi ? &next_norm : nullptr));
         if (!fs->norm_epi)
@@ -612,7 +707,10 @@ static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S
         }
     }
     charge(ctx, fs, NS_LOGITS);
-    KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_PLAIN, fs->xn, mp->out_w, fs->logits, S, V, D, V, 0, cu, fs->gemm_work, kGemmWorkElems));
+    if (streamed)
+        KTRY(ctx, KID_F_GEMM, stream_product(st, fs, vk::STREAM_PLAIN, xn, fs->out_t, fs->logits, S, V, D, V));
+    else
+        KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_PLAIN, fs->xn, mp->out_w, fs->logits, S, V, D, V, 0, cu, fs->gemm_work, kGemmWorkElems));
     charge(ctx, fs, NS_OUTPUT);
     KTRY(ctx, KID_F_ARGMAX, vk::launch_argmax_rows(st, fs->logits, fs->ids, S, V));
     return VKLLM_ERR_OK;
@@ -861,6 +959,51 @@ extern "C" vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *ctx, st
     if (e != hipSuccess)
         return hip_fail(e, "vkllm_hip_model_time_kernel", __FILE__, __LINE__);
     *total_ns = (uint64_t)((double)ms * 1e6);
+    return VKLLM_ERR_OK;
+}
+
+extern "C" vkllm_err_t vkllm_hip_gemm_streamed(struct vkllm_context *ctx, int epi, const uint16_t *A,
+                                               const uint16_t *B, uint16_t *C, uint32_t M, uint32_t N, uint32_t K,
+                                               uint32_t ldc, uint32_t splits)
+{
+    _CHECK_ARGS(ctx && A && B && C && M > 0 && M <= 128 && N > 0 && K >= 16 && K % 16 == 0 && splits <= 8);
+    _CHECK_ARGS(epi == vk::GEMM_PLAIN || epi == vk::GEMM_RESID || epi == vk::GEMM_SWIGLU);
+    _CHECK_ARGS(epi == vk::GEMM_PLAIN ? ldc >= N : (epi == vk::GEMM_RESID ? ldc == N && N % 32 == 0 : N % 32 == 0 && ldc >= N / 2));
+    _CHECK_ARGS(((uintptr_t)A | (uintptr_t)B) % 16 == 0 && (uintptr_t)C % 8 == 0 && ldc % 4 == 0);
+    hipStream_t st = ctx->device->stream;
+    const uint32_t F = epi == vk::GEMM_SWIGLU ? N / 2 : 0;
+    const size_t xt_elems = (size_t)128 * K, wt_elems = vk::stream_tiled_elems(N, K, F);
+    const size_t work_elems = epi == vk::GEMM_RESID ? (size_t)8 * M * N : 0;
+    uint16_t *xt = nullptr, *wt = nullptr;
+    float *work = nullptr;
+    hipError_t e = hipMalloc(&xt, xt_elems * 2);
+    if (e == hipSuccess)
+        e = hipMalloc(&wt, wt_elems * 2);
+    if (e == hipSuccess && work_elems)
+        e = hipMalloc(&work, work_elems * sizeof(float));
+    if (e == hipSuccess)
+        e = vk::launch_tile_activations(st, A, xt, M, K);
+    if (e == hipSuccess)
+        e = vk::launch_tile_weights(st, B, wt, N, K, F);
+    if (e == hipSuccess)
+    {
+        const int sepi = epi == vk::GEMM_PLAIN ? vk::STREAM_PLAIN
+                                                : (epi == vk::GEMM_RESID ? vk::STREAM_PARTIAL : vk::STREAM_SWIGLU);
+        e = timed(ctx, pipeline_of(ctx, KID_F_GEMM), [&]() {
+            uint32_t n_splits = splits;
+            hipError_t r = vk::launch_stream_gemm(st, sepi, xt, wt, C, work, work_elems, M, N, K, ldc, &n_splits);
+            if (r != hipSuccess || sepi != vk::STREAM_PARTIAL)
+                return r;
+            return vk::launch_gemm_reduce(st, vk::GEMM_RESID, work, C, M, N, n_splits);
+        });
+    }
+    if (e == hipSuccess)
+        e = hipStreamSynchronize(st);
+    (void)hipFree(xt);
+    (void)hipFree(wt);
+    (void)hipFree(work);
+    if (e != hipSuccess)
+        return hip_fail(e, "vkllm_hip_gemm_streamed", __FILE__, __LINE__);
     return VKLLM_ERR_OK;
 }
 

@@ -57,7 +57,8 @@ __device__ __forceinline__ float row4_sum(float v)
 template <int HD>
 __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *q, const uint16_t *kc,
                                                                 const uint16_t *vc, uint16_t *out, uint32_t offset,
-                                                                uint32_t S, uint32_t H, uint32_t ctx, float scale)
+                                                                uint32_t S, uint32_t H, uint32_t ctx, float scale,
+                                                                bool xt)
 {
     constexpr int KS = HD / 32;           // 32-wide slices of the head dims (K of S^T = K . Q^T)
     constexpr int DB = HD / 16;           // 16-wide blocks of output dims
@@ -337,7 +338,11 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
         for (int d = 0; d < DB; ++d)
         {
             const uint2 w = {pack2(f2h(o[d][0]), f2h(o[d][1])), pack2(f2h(o[d][2]), f2h(o[d][3]))};
-            *(uint2 *)(orow + 16 * d + 4 * q4) = w;
+            // column h HD + 16 d + 4 q4: in fragment order the 4 halfs sit in the second half of vector kv when q4 is
+            // odd
+            const uint32_t col = h * HD + 16 * d + 4 * q4;
+            uint16_t *dst = xt ? out + (size_t)xt_vec(row, col / 8) * 8 + col % 8 : orow + 16 * d + 4 * q4;
+            *(uint2 *)dst = w;
         }
     }
 }
@@ -350,7 +355,8 @@ template <int HD> constexpr size_t pf_lds_bytes()
 
 template <int HD>
 static hipError_t launch_pf_hd(hipStream_t st, dim3 grid, const uint16_t *q, const uint16_t *kc, const uint16_t *vc,
-                               uint16_t *out, uint32_t offset, uint32_t S, uint32_t H, uint32_t ctx, float scale)
+                               uint16_t *out, uint32_t offset, uint32_t S, uint32_t H, uint32_t ctx, float scale,
+                               bool xt)
 {
     static bool attr_set = false; // LDS beyond the default 64 KB needs the attribute, once per kernel
     constexpr size_t lds = pf_lds_bytes<HD>();
@@ -362,7 +368,7 @@ static hipError_t launch_pf_hd(hipStream_t st, dim3 grid, const uint16_t *q, con
             return e;
         attr_set = true;
     }
-    attn_prefill_mfma_kernel<HD><<<grid, 256, lds, st>>>(q, kc, vc, out, offset, S, H, ctx, scale);
+    attn_prefill_mfma_kernel<HD><<<grid, 256, lds, st>>>(q, kc, vc, out, offset, S, H, ctx, scale, xt);
     return hipGetLastError();
 }
 
@@ -373,14 +379,14 @@ bool attn_prefill_mfma_ok(uint32_t hd)
 
 hipError_t launch_attn_prefill_mfma(hipStream_t st, const uint16_t *q, const uint16_t *kc, const uint16_t *vc,
                                     uint16_t *out, uint32_t offset, uint32_t S, uint32_t H, uint32_t hd, uint32_t ctx,
-                                    float scale)
+                                    float scale, bool xt)
 {
-    if (S == 0 || offset + S > ctx || !attn_prefill_mfma_ok(hd))
+    if (S == 0 || offset + S > ctx || !attn_prefill_mfma_ok(hd) || (xt && S > 128))
         return hipErrorInvalidValue;
     const dim3 grid((S + kPfRows - 1) / kPfRows, H);
     if (hd == 128)
-        return launch_pf_hd<128>(st, grid, q, kc, vc, out, offset, S, H, ctx, scale);
-    return launch_pf_hd<64>(st, grid, q, kc, vc, out, offset, S, H, ctx, scale);
+        return launch_pf_hd<128>(st, grid, q, kc, vc, out, offset, S, H, ctx, scale, xt);
+    return launch_pf_hd<64>(st, grid, q, kc, vc, out, offset, S, H, ctx, scale, xt);
 }
 
 } // namespace vk

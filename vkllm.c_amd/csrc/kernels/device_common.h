@@ -178,9 +178,25 @@ __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi)
     return (uint32_t)lo | ((uint32_t)hi << 16);
 }
 
-// normalises row `x` (D fp16) into `dst` (8 halfs per u32x4); all threads of the block take part
+// fp16(fp16(up) * fp16(silu(gate))) as the reference's ffn_up_and_gate rounds it
+__device__ __forceinline__ uint16_t swiglu_out(float up, float gate)
+{
+    return f2h(h2f(f2h(up)) * h2f(f2h(silu(gate))));
+}
+
+// Prompt-step activations of at most 128 rows (tokens) kept in the operand order of v_mfma_f32_32x32x16_f16's B
+// matrix over 32-token blocks, so a wave reads one 16-K step of one token block as 1 KB contiguous: the 16-byte
+// vector holding row t, columns 8 kv .. 8 kv + 7 of an [M <= 128, K] fp16 matrix is vector number
+// (kv / 2 * 4 + t / 32) * 64 + (kv % 2) * 32 + t % 32. The matrix takes 128 * K halfs whatever M is.
+__device__ __forceinline__ uint32_t xt_vec(uint32_t t, uint32_t kv)
+{
+    return ((kv / 2) * 4 + t / 32) * 64 + (kv % 2) * 32 + t % 32;
+}
+
+// normalises row `x` (D fp16) into `dst` (8 halfs per u32x4); all threads of the block take part. With
+// xt_row >= 0, dst is a fragment-ordered activation matrix (xt_vec) and the row is its row xt_row.
 __device__ __forceinline__ void rmsnorm_row_to(const uint16_t *x, const float *w, u32x4 *dst, uint32_t D, float eps,
-                                               float *red)
+                                               float *red, int xt_row = -1)
 {
     const uint32_t nv = D / 8;
     const u32x4 *xv = (const u32x4 *)x;
@@ -211,7 +227,7 @@ __device__ __forceinline__ void rmsnorm_row_to(const uint16_t *x, const float *w
             float a = half_lo(v[k]), b = half_hi(v[k]);
             o[k] = pack2(f2h((a * ws[2 * k]) * alpha), f2h((b * ws[2 * k + 1]) * alpha));
         }
-        dst[i] = o;
+        dst[xt_row < 0 ? i : xt_vec((uint32_t)xt_row, i)] = o;
     }
 }
 

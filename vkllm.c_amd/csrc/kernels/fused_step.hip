@@ -89,17 +89,22 @@ hipError_t launch_embed_decode(hipStream_t st, const DecodeIo *io, Step *step, c
 
 // 512 threads a row, the block size of the norm fused into the residual products' split-K reduce (same sum order)
 __global__ __launch_bounds__(512) void rmsnorm_rows_kernel(const uint16_t *x, const float *w, uint16_t *y, uint32_t D,
-                                                           float eps)
+                                                           float eps, bool xt)
 {
     __shared__ float red[8];
     const size_t s = blockIdx.x;
-    rmsnorm_row_to(x + s * D, w, (u32x4 *)(y + s * D), D, eps, red);
+    if (xt)
+        rmsnorm_row_to(x + s * D, w, (u32x4 *)y, D, eps, red, (int)s);
+    else
+        rmsnorm_row_to(x + s * D, w, (u32x4 *)(y + s * D), D, eps, red);
 }
 
 hipError_t launch_rmsnorm_rows(hipStream_t st, const uint16_t *x, const float *w, uint16_t *y, uint32_t S,
-                               uint32_t D, float eps)
+                               uint32_t D, float eps, bool xt)
 {
-    rmsnorm_rows_kernel<<<S, 512, 0, st>>>(x, w, y, D, eps);
+    if (xt && (S > 128 || D % 16 != 0))
+        return hipErrorInvalidValue;
+    rmsnorm_rows_kernel<<<S, 512, 0, st>>>(x, w, y, D, eps, xt);
     return hipGetLastError();
 }
 
@@ -731,12 +736,14 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t *q, co
 
 hipError_t launch_attn_prefill(hipStream_t st, const uint16_t *q, const uint16_t *kc, const uint16_t *vc,
                                uint16_t *out, uint32_t offset, uint32_t S, uint32_t H, uint32_t hd, uint32_t ctx,
-                               float scale)
+                               float scale, bool xt)
 {
     if (hd % 8 != 0 || hd > 256)
         return hipErrorInvalidValue;
     if (attn_prefill_mfma_ok(hd))
-        return launch_attn_prefill_mfma(st, q, kc, vc, out, offset, S, H, hd, ctx, scale);
+        return launch_attn_prefill_mfma(st, q, kc, vc, out, offset, S, H, hd, ctx, scale, xt);
+    if (xt) // fragment-ordered output from the MFMA kernel only
+        return hipErrorInvalidValue;
     const size_t lds = (size_t)(offset + S) * sizeof(float);
     attn_prefill_kernel<<<dim3(S, H), 256, lds, st>>>(q, kc, vc, out, offset, S, H, hd, ctx, scale);
     return hipGetLastError();

@@ -59,11 +59,6 @@ __device__ __forceinline__ uint32_t swiglu_col(uint32_t c)
 {
     return 32 * (c / 64) + c % 32;
 }
-// fp16(fp16(up) * fp16(silu(gate))) as the reference's ffn_up_and_gate rounds it
-__device__ __forceinline__ uint16_t swiglu_out(float up, float gate)
-{
-    return f2h(h2f(f2h(up)) * h2f(f2h(silu(gate))));
-}
 
 // GEMM_QKV_ROPE: element (m, c) of region `region` (0 q, 1 k, 2 v) at head `head`, head dim `dim`; v is the
 // element's fp16-rounded value and w its RoPE partner's (dim ^ 1), as launch_rope_kv combines them
@@ -628,7 +623,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float *wo
 // sum order). Each thread re-reads only the vectors it wrote.
 __global__ __launch_bounds__(512) void gemm_resid_norm_kernel(const float *work, uint16_t *C, uint32_t M, uint32_t N,
                                                               uint32_t splits, const float *w, uint16_t *y,
-                                                              float eps)
+                                                              float eps, bool xt)
 {
     __shared__ float red[8];
     const uint32_t m = blockIdx.x, nv = N / 8;
@@ -658,7 +653,10 @@ __global__ __launch_bounds__(512) void gemm_resid_norm_kernel(const float *work,
             o[k] = pack2(f2h(half_lo(r[k]) + h2f(f2h(acc[2 * k]))), f2h(half_hi(r[k]) + h2f(f2h(acc[2 * k + 1]))));
         cv[i] = o;
     }
-    rmsnorm_row_to(C + (size_t)m * N, w, (u32x4 *)(y + (size_t)m * N), N, eps, red);
+    if (xt)
+        rmsnorm_row_to(C + (size_t)m * N, w, (u32x4 *)y, N, eps, red, (int)m);
+    else
+        rmsnorm_row_to(C + (size_t)m * N, w, (u32x4 *)(y + (size_t)m * N), N, eps, red);
 }
 
 template <int BM, int BN> static size_t gemm_lds()
@@ -828,7 +826,8 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
                 if (e != hipSuccess)
                     return e;
                 // 512 threads a row (one 16-byte vector each at width 4096) keep a row's partial loads in flight
-                gemm_resid_norm_kernel<<<M, 512, 0, st>>>(work, C, M, N, splits, norm->w, norm->y, norm->eps);
+                gemm_resid_norm_kernel<<<M, 512, 0, st>>>(work, C, M, N, splits, norm->w, norm->y, norm->eps,
+                                                          norm->xt);
                 *normed = true;
                 return hipGetLastError();
             }
@@ -857,6 +856,29 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
     }
 }
 
+hipError_t launch_gemm_reduce(hipStream_t st, int epi, const float *work, uint16_t *C, uint32_t M, uint32_t N,
+                              uint32_t splits, const GemmRope *rope, const GemmNorm *norm)
+{
+    if (M == 0 || N == 0 || splits == 0)
+        return hipErrorInvalidValue;
+    switch (epi)
+    {
+    case GEMM_RESID:
+        if (!norm)
+            return launch_reduce<GEMM_RESID>(st, work, C, M, N, N, 0, splits, 0, nullptr);
+        if (N % 8 != 0 || (norm->xt && (M > 128 || N % 16 != 0)))
+            return hipErrorInvalidValue;
+        gemm_resid_norm_kernel<<<M, 512, 0, st>>>(work, C, M, N, splits, norm->w, norm->y, norm->eps, norm->xt);
+        return hipGetLastError();
+    case GEMM_QKV_ROPE:
+        if (!rope || N != 3 * rope->D)
+            return hipErrorInvalidValue;
+        return launch_reduce<GEMM_QKV_ROPE>(st, work, C, M, N, N, 0, splits, 0, rope);
+    default:
+        return hipErrorInvalidValue;
+    }
+}
+
 hipError_t launch_gemm(hipStream_t st, int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, uint32_t M,
                        uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, int cu_count, float *work,
                        size_t work_elems, const GemmRope *rope, const GemmNorm *norm)
@@ -880,7 +902,7 @@ hipError_t launch_gemm(hipStream_t st, int epi, const uint16_t *A, const uint16_
                                                    nullptr, norm, &normed);
         if (e != hipSuccess || !norm || normed)
             return e;
-        return launch_rmsnorm_rows(st, C, norm->w, norm->y, M, N, norm->eps);
+        return launch_rmsnorm_rows(st, C, norm->w, norm->y, M, N, norm->eps, norm->xt);
     }
     case GEMM_SWIGLU:
         return launch_epi_gemm<GEMM_SWIGLU>(st, A, B, C, work, work_elems, M, N, K, ldc, split, cu_count, nullptr,

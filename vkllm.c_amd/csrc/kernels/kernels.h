@@ -63,9 +63,9 @@ hipError_t launch_embed_decode(hipStream_t st, const DecodeIo *io, Step *step, c
 // h[s] = embd[toks[s]] (ids >= V read row unk), s < S; D % 8 == 0
 hipError_t launch_embed_rows(hipStream_t st, const uint32_t *toks, uint32_t S, const uint16_t *embd, uint16_t *h,
                              uint32_t V, uint32_t D, uint32_t unk);
-// y[s] = rmsnorm(x[s]) * w, s < S
+// y[s] = rmsnorm(x[s]) * w, s < S; with xt, y is fragment-ordered (xt_vec; S <= 128, D % 16 == 0)
 hipError_t launch_rmsnorm_rows(hipStream_t st, const uint16_t *x, const float *w, uint16_t *y, uint32_t S,
-                               uint32_t D, float eps);
+                               uint32_t D, float eps, bool xt = false);
 
 enum GemvEpi : int
 {
@@ -157,12 +157,13 @@ hipError_t launch_attn_o(hipStream_t st, const AttnOArgs &a, uint32_t kv_max, in
 // prefill: queries s < S at positions offset+s attend to positions <= offset+s (the row max over all offset+S);
 // head sizes 64 and 128 run on the MFMA kernel, others one workgroup per (row, head)
 bool attn_prefill_mfma_ok(uint32_t hd);
+// with xt, out is fragment-ordered (xt_vec; S <= 128)
 hipError_t launch_attn_prefill_mfma(hipStream_t st, const uint16_t *q, const uint16_t *kc, const uint16_t *vc,
                                     uint16_t *out, uint32_t offset, uint32_t S, uint32_t H, uint32_t hd, uint32_t ctx,
-                                    float scale);
+                                    float scale, bool xt = false);
 hipError_t launch_attn_prefill(hipStream_t st, const uint16_t *q, const uint16_t *kc, const uint16_t *vc,
                                uint16_t *out, uint32_t offset, uint32_t S, uint32_t H, uint32_t hd, uint32_t ctx,
-                               float scale);
+                               float scale, bool xt = false);
 // qkv [S, 3D] -> RoPE'd q [S, D]; RoPE'd k and v into the caches at rows offset..offset+S-1
 hipError_t launch_rope_kv(hipStream_t st, const uint16_t *qkv, uint16_t *q, uint16_t *kc, uint16_t *vc,
                           const float *freqs, uint32_t offset, uint32_t S, uint32_t D, uint32_t hd, uint32_t ctx);
@@ -195,12 +196,14 @@ struct GemmRope
     const float *cs;     // [M][hd / 2][2]: cos and sin of (offset + m) / base^(2w/hd), from launch_rope_table
     uint32_t offset, D, hd, ctx;
 };
-// GEMM_RESID followed by y[m] = RMSNorm(C[m]) * w (ldc == N; the norm of launch_rmsnorm_rows)
+// GEMM_RESID followed by y[m] = RMSNorm(C[m]) * w (ldc == N; the norm of launch_rmsnorm_rows); with xt, y is
+// fragment-ordered (xt_vec; M <= 128)
 struct GemmNorm
 {
     const float *w;
     uint16_t *y;
     float eps;
+    bool xt = false;
 };
 // C[M, N] (row stride ldc) = A[M, K] . B[N, K]^T, fp16 operands, fp32 accumulation on MFMA. K % 8 == 0.
 // `work` (work_elems floats) holds split-K partial tiles for short prompts; with too little of it K is not split.
@@ -209,6 +212,28 @@ struct GemmNorm
 hipError_t launch_gemm(hipStream_t st, int epi, const uint16_t *A, const uint16_t *B, uint16_t *C, uint32_t M,
                        uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, int cu_count, float *work,
                        size_t work_elems, const GemmRope *rope = nullptr, const GemmNorm *norm = nullptr);
+// Prompt-step products of at most 128 tokens with the weights read from a fragment-tiled copy (launch_tile_weights)
+// and X fragment-ordered (xt_vec): C[M, N] = X[M, K] . W[N, K]^T, M <= 128, K % 16 == 0.
+enum StreamEpi : int
+{
+    STREAM_PARTIAL = 0, // work[z][M][N]: fp32 partials of K range z (N % 32 == 0), for launch_gemm_reduce
+    STREAM_PLAIN = 1,   // C[m][n] = fp16(acc), row stride ldc
+    STREAM_SWIGLU = 2,  // the interleaved [Wu; Wg] copy (N = 2F): C[m][f] = fp16(fp16(up) * fp16(silu(gate)))
+};
+// halfs of the tiled copy of W [N, K] (F > 0: [Wu; Wg] with N = 2F, F % 16 == 0, rows interleaved in 16s)
+size_t stream_tiled_elems(uint32_t N, uint32_t K, uint32_t F);
+hipError_t launch_tile_weights(hipStream_t st, const uint16_t *W, uint16_t *Wt, uint32_t N, uint32_t K, uint32_t F);
+// row-major X [M <= 128, K] -> fragment order (128 * K halfs, rows past M zero)
+hipError_t launch_tile_activations(hipStream_t st, const uint16_t *X, uint16_t *Xt, uint32_t M, uint32_t K);
+// *splits: K ranges wanted for STREAM_PARTIAL (0: enough for about one workgroup per CU); on return the ranges used
+// (1 for the other epilogues). work holds work_elems floats.
+hipError_t launch_stream_gemm(hipStream_t st, int epi, const uint16_t *X, const uint16_t *Wt, uint16_t *C,
+                              float *work, size_t work_elems, uint32_t M, uint32_t N, uint32_t K, uint32_t ldc,
+                              uint32_t *splits);
+// The epilogue of split-K partials work[z][M][N] (z < splits, added in order), as launch_gemm applies it: GEMM_RESID
+// (C += the sum; with `norm`, the rows' RMSNorm as well) or GEMM_QKV_ROPE (`rope`'s q and caches).
+hipError_t launch_gemm_reduce(hipStream_t st, int epi, const float *work, uint16_t *C, uint32_t M, uint32_t N,
+                              uint32_t splits, const GemmRope *rope = nullptr, const GemmNorm *norm = nullptr);
 // Looks up the device address of the allocation-free GEMM's scratch array on device `dev` (current), once per
 // device; vkllm_context_new calls it.
 hipError_t noalloc_scratch_init(int dev);

@@ -216,6 +216,7 @@ def lib():
             "vkllm_hip_token_loop": (E, [vp, ctypes.POINTER(ModelStruct), vp, u32, u32, u32, vp, vp, vp]),
             "vkllm_hip_gemm": (E, [vp, E, vp, vp, vp, u32, u32, u32, u32, u32, vp, ctypes.c_uint64]),
             "vkllm_hip_gemm_noalloc": (E, [vp, E, vp, vp, vp, u32, u32, u32, u32, u32, ctypes.c_uint64]),
+            "vkllm_hip_gemm_streamed": (E, [vp, E, vp, vp, vp, u32, u32, u32, u32, u32]),
             "vkllm_hip_abi_layout": (E, [ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_uint64), E]),
             "vkllm_hashmap_new": (E, [ctypes.POINTER(vp), ctypes.c_size_t]),
             "vkllm_hashmap_free": (None, [vp]),
