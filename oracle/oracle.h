@@ -8,7 +8,8 @@
  * cites the reference file:line it follows (paths relative to the vkllm.c tree).
  *
  * Numerics mode: fp16 storage, fp32 arithmetic -- the variant the reference selects when the device has 16-bit
- * storage but no fp16 arithmetic (src/core/vkllm_op_matmul.c:103-113, src/shaders/BUILD:82,102,121,141).
+ * storage but no fp16 arithmetic (src/core/vkllm_op_matmul.c:103-113, src/shaders/BUILD:82,102,121,141). A second
+ * mode (REF16, oracle_set_numerics below) restates the fp16-arithmetic variants to measure how far they drift.
  * Every graph node's output is rounded to its storage dtype (fp16 round-to-nearest-even), exactly where the
  * reference's graph materialises a tensor. Reductions (dot products, sums of squares, softmax sums) are
  * accumulated in double and rounded once to fp32: the reference's fp32 summation order is decided by the
@@ -105,6 +106,37 @@ int oracle_arg_max(const oracle_tensor *in, oracle_tensor *out);
 /* VKLLM_OP_FFN_UP_AND_GATE: out = (x.Wu^T) * silu(x.Wg^T); src/shaders/vkllm_ffn_up_and_gate.comp:44-149 */
 int oracle_ffn_up_and_gate(const oracle_tensor *x, const oracle_tensor *wu, const oracle_tensor *wg,
                            oracle_tensor *out);
+
+/* ---- REF16: the reference's fp16-arithmetic shader variants ----
+ * With fp16 arithmetic on the device the reference selects the f16f16 variants (src/core/vkllm_op_matmul.c:92-101,
+ * src/core/vkllm_op_rope.c:22, src/core/vkllm_op_softmax.c:24; macros at src/shaders/BUILD:81,101,120,140) instead
+ * of the fp32-arithmetic ones this build follows. The residual adds and the up * gate product (bin_op f16f16f16,
+ * src/shaders/BUILD:24) round one fp16 operation and RMSNorm has no fp16-arithmetic variant (BUILD:55-68), so those
+ * are as in the fp32 mode. REF16
+ * restates them: every arithmetic operation on fp16 values rounds its exact result once to fp16 (round to nearest
+ * even; fp16 exp, cos, sin and pow are the correctly rounded values), and the driver-defined parts take one fixed
+ * choice: subgroupAdd adds the lanes in order, dot(f16vec2) is fp16(fp16(a0 b0) + fp16(a1 b1)), and dot(vec4) in
+ * fp32 adds the four products in order. Nothing in the reference pins those choices, so REF16 measures how far an
+ * fp16-arithmetic device's tokens and logits can be from the fp32-arithmetic ones; it is not a bit-exact restatement.
+ * oracle_set_numerics(1, g) switches the model step to it with subgroups of g lanes (lavapipe's width on the host
+ * CPU; 32 in the shader's comments); oracle_set_numerics(0, 0) restores the fp32 mode. Not thread-safe: set it
+ * between steps. */
+void oracle_set_numerics(int ref16, uint32_t subgroup);
+/* fp16 round-to-nearest-even of a double (no double rounding through fp32) */
+uint16_t oracle_f64_to_f16(double v);
+/* src/shaders/vkllm_mat_mul_vec.comp:118-146 f16f16: one output of x[K] . w[K] (K % 4 == 0), times scale, SiLU
+ * when act, in fp16 with subgroups of `subgroup` lanes */
+uint16_t oracle_gemv16(const uint16_t *x, const uint16_t *w, uint32_t K, float scale, int act, uint32_t subgroup);
+/* src/shaders/vkllm_matmul_t1.comp:202-221 f16f16f16: sum over k pairs of fp16 dot(f16vec2), accumulated in fp32
+ * (an odd K pads the last pair with 0); returns the fp32 sum */
+float oracle_gemm16_dot(const uint16_t *a, const uint16_t *b, uint32_t K);
+/* src/shaders/vkllm_softmax.comp:53-95 f16f16 on one row of W fp16 values: entries i > limit masked (limit >= W:
+ * none) */
+void oracle_softmax16_row(const uint16_t *x, uint16_t *out, uint32_t W, uint32_t limit, uint32_t subgroup);
+/* src/shaders/vkllm_rope.comp:68-78 f16f16: pair (v0, v1) at dims (2w, 2w + 1) of a head of size hd at position
+ * pos rotated with fp16 angle arithmetic */
+void oracle_rope16_pair(uint16_t v0, uint16_t v1, uint32_t pos, uint32_t w, uint32_t hd, float base, uint16_t *o0,
+                        uint16_t *o1);
 
 /* ---- LLaMA-2 model ---- */
 typedef struct

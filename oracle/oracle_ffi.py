@@ -89,8 +89,59 @@ def lib():
                                         ctypes.c_void_p]
         L.oracle_token_loop.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32), ctypes.c_uint32,
                                         ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint32), ctypes.c_void_p]
+        L.oracle_set_numerics.argtypes = [ctypes.c_int, ctypes.c_uint32]
+        L.oracle_f64_to_f16.restype = ctypes.c_uint16
+        L.oracle_f64_to_f16.argtypes = [ctypes.c_double]
+        L.oracle_gemv16.restype = ctypes.c_uint16
+        L.oracle_gemv16.argtypes = [P16, P16, ctypes.c_uint32, ctypes.c_float, ctypes.c_int, ctypes.c_uint32]
+        L.oracle_gemm16_dot.restype = ctypes.c_float
+        L.oracle_gemm16_dot.argtypes = [P16, P16, ctypes.c_uint32]
+        L.oracle_softmax16_row.argtypes = [P16, P16, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32]
+        L.oracle_rope16_pair.argtypes = [ctypes.c_uint16, ctypes.c_uint16, ctypes.c_uint32, ctypes.c_uint32,
+                                         ctypes.c_uint32, ctypes.c_float, P16, P16]
         _lib = L
     return _lib
+
+
+P16 = ctypes.POINTER(ctypes.c_uint16)
+
+
+def _p16(a):
+    return a.ctypes.data_as(P16)
+
+
+def set_numerics(ref16, subgroup=8):
+    """REF16 (the reference's fp16-arithmetic shader variants, subgroups of `subgroup` lanes) or the fp32 mode"""
+    lib().oracle_set_numerics(1 if ref16 else 0, subgroup if ref16 else 0)
+
+
+def f64_to_f16_bits(x):
+    return lib().oracle_f64_to_f16(float(x))
+
+
+def gemv16(x, w, scale=1.0, act=0, subgroup=8):
+    x = np.ascontiguousarray(x, np.uint16)
+    w = np.ascontiguousarray(w, np.uint16)
+    return lib().oracle_gemv16(_p16(x), _p16(w), len(x), scale, act, subgroup)
+
+
+def gemm16_dot(a, b):
+    a = np.ascontiguousarray(a, np.uint16)
+    b = np.ascontiguousarray(b, np.uint16)
+    return lib().oracle_gemm16_dot(_p16(a), _p16(b), len(a))
+
+
+def softmax16_row(x, limit=None, subgroup=8):
+    x = np.ascontiguousarray(x, np.uint16)
+    out = np.zeros_like(x)
+    lib().oracle_softmax16_row(_p16(x), _p16(out), len(x), len(x) if limit is None else limit, subgroup)
+    return out
+
+
+def rope16_pair(v0, v1, pos, w, hd, base=10000.0):
+    o0, o1 = ctypes.c_uint16(), ctypes.c_uint16()
+    lib().oracle_rope16_pair(v0, v1, pos, w, hd, base, ctypes.byref(o0), ctypes.byref(o1))
+    return o0.value, o1.value
 
 
 def tensor(arr, shapes=None, strides=None, dtype=None):

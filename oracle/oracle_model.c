@@ -747,6 +747,149 @@ const uint16_t *oracle_model_weight(const oracle_model *m, uint32_t id, size_t *
 }
 
 /* ------------------------------------------------------------------------------------------------------------ */
+/* REF16: fp16 arithmetic of the reference's f16f16 shader variants (declared with their citations in oracle.h) */
+
+static int g_ref16 = 0;
+static uint32_t g_sub = 8;
+
+void oracle_set_numerics(int ref16, uint32_t subgroup)
+{
+    g_ref16 = ref16 != 0;
+    g_sub = subgroup ? subgroup : 8;
+}
+
+uint16_t oracle_f64_to_f16(double d)
+{
+    uint64_t x;
+    memcpy(&x, &d, 8);
+    const uint16_t sign = (uint16_t)((x >> 48) & 0x8000u);
+    const int exp = (int)((x >> 52) & 0x7ffu);
+    const uint64_t mant = x & 0xfffffffffffffull;
+    if (exp == 0x7ff)
+        return (uint16_t)(sign | (mant ? 0x7e00u : 0x7c00u));
+    if (exp == 0) /* zero, or a double subnormal: far below half the smallest fp16 subnormal */
+        return sign;
+    const int e = exp - 1023;
+    if (e > 15)
+        return (uint16_t)(sign | 0x7c00u);
+    if (e < -25) /* below half of 2^-24 */
+        return sign;
+    const uint64_t full = mant | (1ull << 52); /* value = full * 2^(e - 52) */
+    /* kept bits: 11 for a normal result (exponent >= -14), fewer for a subnormal one (units of 2^-24) */
+    const int shift = e >= -14 ? 42 : 42 + (-14 - e);
+    uint64_t m = full >> shift;
+    const uint64_t rem = full & ((1ull << shift) - 1), half = 1ull << (shift - 1);
+    if (rem > half || (rem == half && (m & 1u)))
+        ++m;
+    if (e < -14) /* subnormal; a carry into 0x400 is the smallest normal, the same bits */
+        return (uint16_t)(sign | (uint16_t)m);
+    uint32_t hexp = (uint32_t)(e + 15);
+    if (m == 0x800u)
+    {
+        m = 0x400u;
+        ++hexp;
+    }
+    if (hexp >= 31)
+        return (uint16_t)(sign | 0x7c00u);
+    return (uint16_t)(sign | (hexp << 10) | (uint32_t)(m & 0x3ffu));
+}
+
+/* the exact result of one fp16 operation, rounded to fp16 and read back */
+static inline float r16(double v)
+{
+    return h2f(oracle_f64_to_f16(v));
+}
+
+/* exp, cos, sin and pow of fp16 arguments as correctly rounded fp16 values */
+static inline float exp16(float v)
+{
+    return r16(exp((double)v));
+}
+
+static float gemv16_value(const uint16_t *x, const uint16_t *w, uint32_t K, float scale, int act, uint32_t G)
+{
+    float total = 0.f;
+    for (uint32_t l = 0; l < G; ++l)
+    {
+        /* lane l: fp16 accumulator += fp16(dot(vec4 a, vec4 b) in fp32) for i = 4l, 4l + 4G, ... */
+        float acc = 0.f;
+        for (uint32_t i = 4 * l; i + 3 < K; i += 4 * G)
+        {
+            float d = h2f(x[i]) * h2f(w[i]);
+            d = d + h2f(x[i + 1]) * h2f(w[i + 1]);
+            d = d + h2f(x[i + 2]) * h2f(w[i + 2]);
+            d = d + h2f(x[i + 3]) * h2f(w[i + 3]);
+            acc = r16((double)r16(d) + acc);
+        }
+        /* subgroupAdd in fp16, lanes in order */
+        total = l == 0 ? acc : r16((double)total + acc);
+    }
+    float v = r16((double)total * r16(scale));
+    if (act) /* v / (1 + exp(-v)) in fp16 */
+        v = r16((double)v / r16(1.0 + exp16(r16(-(double)v))));
+    return v;
+}
+
+uint16_t oracle_gemv16(const uint16_t *x, const uint16_t *w, uint32_t K, float scale, int act, uint32_t subgroup)
+{
+    pthread_once(&g_h2f_once, h2f_init);
+    return oracle_f32_to_f16(gemv16_value(x, w, K, scale, act, subgroup ? subgroup : 8));
+}
+
+/* fp16 dot(f16vec2) of pairs read with element strides sa, sb, accumulated in fp32 */
+static float gemm16_dot_strided(const uint16_t *a, size_t sa, const uint16_t *b, size_t sb, uint32_t K)
+{
+    float acc = 0.f;
+    for (uint32_t k = 0; k < K; k += 2)
+    {
+        const float p0 = r16((double)h2f(a[k * sa]) * h2f(b[k * sb]));
+        const float p1 = k + 1 < K ? r16((double)h2f(a[(k + 1) * sa]) * h2f(b[(k + 1) * sb])) : 0.f;
+        acc += r16((double)p0 + p1);
+    }
+    return acc;
+}
+
+float oracle_gemm16_dot(const uint16_t *a, const uint16_t *b, uint32_t K)
+{
+    pthread_once(&g_h2f_once, h2f_init);
+    return gemm16_dot_strided(a, 1, b, 1, K);
+}
+
+void oracle_softmax16_row(const uint16_t *x, uint16_t *out, uint32_t W, uint32_t limit, uint32_t subgroup)
+{
+    pthread_once(&g_h2f_once, h2f_init);
+    const uint32_t G = subgroup ? subgroup : 8;
+    float mx = h2f(x[0]); /* the max over the whole row, masked entries included: exact in any precision */
+    for (uint32_t i = 0; i < W; ++i)
+        mx = h2f(x[i]) > mx ? h2f(x[i]) : mx;
+    float total = 0.f;
+    for (uint32_t l = 0; l < G; ++l)
+    {
+        float acc = 0.f;
+        for (uint32_t i = l; i < W; i += G)
+            if (i <= limit)
+                acc = r16((double)acc + exp16(r16((double)h2f(x[i]) - mx)));
+        total = l == 0 ? acc : r16((double)total + acc);
+    }
+    for (uint32_t i = 0; i < W; ++i)
+        out[i] = i > limit ? 0 : oracle_f64_to_f16((double)exp16(r16((double)h2f(x[i]) - mx)) / total);
+}
+
+void oracle_rope16_pair(uint16_t v0, uint16_t v1, uint32_t pos, uint32_t w, uint32_t hd, float base, uint16_t *o0,
+                        uint16_t *o1)
+{
+    pthread_once(&g_h2f_once, h2f_init);
+    /* f = fp16(pos) / pow(fp16(base), fp16(2w) / fp16(hd)), each operation in fp16 */
+    const float e = r16((double)r16(2.0 * w) / r16((double)hd));
+    const float pw = r16(pow((double)r16((double)base), (double)e));
+    const float f = r16((double)r16((double)pos) / pw);
+    const float c = r16(cos((double)f)), sn = r16(sin((double)f));
+    const float a = h2f(v0), b = h2f(v1);
+    *o0 = oracle_f64_to_f16((double)r16((double)c * a) - r16((double)sn * b));
+    *o1 = oracle_f64_to_f16((double)r16((double)sn * a) + r16((double)c * b));
+}
+
+/* ------------------------------------------------------------------------------------------------------------ */
 /* forward step */
 
 /* y[s][n] = fp16(act(scale * sum_k x[s][k] W[n][k])): VKLLM_OP_MATMUL with a [N,K] weight
@@ -754,6 +897,7 @@ const uint16_t *oracle_model_weight(const oracle_model *m, uint32_t id, size_t *
 typedef struct
 {
     const double *xd;
+    const uint16_t *x16;
     const uint16_t *W;
     uint16_t *y;
     uint32_t S, K, N;
@@ -765,6 +909,25 @@ static void linear_row(void *p, size_t n)
     const linear_job *j = (const linear_job *)p;
     const uint32_t K = j->K;
     const uint16_t *w = j->W + n * K;
+    if (g_ref16)
+    {
+        /* one token: mat_mul_vec f16f16; more: the tiled GEMM f16f16f16 (fp16 pair dots, fp32 sum and epilogue) */
+        for (uint32_t s = 0; s < j->S; ++s)
+        {
+            const uint16_t *xs = j->x16 + (size_t)s * K;
+            float v;
+            if (j->S == 1)
+                v = gemv16_value(xs, w, K, 1.0f, j->act, g_sub);
+            else
+            {
+                v = oracle_gemm16_dot(xs, w, K) * 1.0f;
+                if (j->act)
+                    v = v / (1.0f + expf(-v));
+            }
+            j->y[(size_t)s * j->N + n] = oracle_f32_to_f16(v);
+        }
+        return;
+    }
     for (uint32_t s = 0; s < j->S; ++s)
     {
         const double *xs = j->xd + (size_t)s * K;
@@ -783,7 +946,7 @@ static void linear(const uint16_t *x, const uint16_t *W, uint16_t *y, uint32_t S
     double *xd = (double *)malloc(sizeof(double) * K * S);
     for (size_t i = 0; i < (size_t)K * S; ++i)
         xd[i] = h2f(x[i]);
-    linear_job j = {xd, W, y, S, K, N, act};
+    linear_job j = {xd, x, W, y, S, K, N, act};
     par_for(N, linear_row, &j, (double)N * S * K);
     free(xd);
 }
@@ -834,6 +997,35 @@ static void attn_row(void *p, size_t i)
     uint16_t *sc = (uint16_t *)malloc((size_t)kv * 2);
     uint16_t *pr = (uint16_t *)malloc((size_t)kv * 2);
     const uint16_t *qr = a->rq + ((size_t)hh * S + s) * hd;
+
+    if (g_ref16)
+    {
+        /* scores: mat_mul_vec f16f16 for one query row, else the tiled GEMM (fp32 scale in its epilogue) */
+        for (uint32_t j = 0; j < kv; ++j)
+        {
+            const uint16_t *kr = kc + ((size_t)hh * ctx + j) * hd;
+            sc[j] = S == 1 ? oracle_gemv16(qr, kr, hd, scale, 0, g_sub)
+                           : oracle_f32_to_f16(oracle_gemm16_dot(qr, kr, hd) * scale);
+        }
+        oracle_softmax16_row(sc, pr, kv, s + offset, g_sub);
+        /* attn . V: the tiled GEMM over key pairs (V read [kv, hd]); when kv == hd, is_transposed_b reads V as
+         * [N, K] and one query row takes mat_mul_vec */
+        const int tr = kv == hd;
+        for (uint32_t n = 0; n < hd; ++n)
+        {
+            float v;
+            if (tr && S == 1)
+                v = gemv16_value(pr, vc + ((size_t)hh * ctx + n) * hd, kv, 1.0f, 0, g_sub);
+            else if (tr)
+                v = gemm16_dot_strided(pr, 1, vc + ((size_t)hh * ctx + n) * hd, 1, kv);
+            else
+                v = gemm16_dot_strided(pr, 1, vc + (size_t)hh * ctx * hd + n, hd, kv);
+            att[(size_t)s * D + (size_t)hh * hd + n] = oracle_f32_to_f16(v * 1.0f);
+        }
+        free(sc);
+        free(pr);
+        return;
+    }
 
     /* scores = fp16(scale * q.k) (src/models/vkllm_llama2_layers.c:223-233) */
     for (uint32_t j = 0; j < kv; ++j)
@@ -922,6 +1114,16 @@ int oracle_model_step(oracle_model *m, const uint32_t *toks, uint32_t S, uint32_
                 for (uint32_t w = 0; w < hd / 2; ++w)
                 {
                     size_t src = (size_t)s * D + (size_t)hh * hd + 2 * w;
+                    if (g_ref16)
+                    {
+                        size_t dq = ((size_t)hh * S + s) * hd + 2 * w;
+                        size_t dk = ((size_t)hh * ctx + offset + s) * hd + 2 * w;
+                        oracle_rope16_pair(q[src], q[src + 1], offset + s, w, hd, c->theta, &rq[dq], &rq[dq + 1]);
+                        oracle_rope16_pair(k[src], k[src + 1], offset + s, w, hd, c->theta, &kc[dk], &kc[dk + 1]);
+                        vc[dk] = v[src];
+                        vc[dk + 1] = v[src + 1];
+                        continue;
+                    }
                     float f = (float)(offset + s) / m->freqs[w];
                     float fc = cosf(f), fs = sinf(f);
                     float q0 = h2f(q[src]), q1 = h2f(q[src + 1]);

@@ -129,3 +129,37 @@ def test_streamed_prefill_against_tile_gemms(ctx, vk, monkeypatch):
     ids_b, logits_b = _device_loop(ctx, vk, shape, 7, prompt, 4)
     assert ids_a.tolist() == ids_b.tolist()
     assert np.max(np.abs(logits_a.astype(np.float32) - logits_b.astype(np.float32))) <= LOGIT_TOL
+
+
+def test_streamed_prefill_in_chunks(ctx, vk, oracle):
+    """A 300-token prompt at the 7B widths (two layers) in chunks of 100, 128 and 72 rows, each a streamed prompt step
+    at a nonzero offset (RoPE angles, K/V rows and causal limits past the first chunk), then 4 decode steps: every
+    row's logits within 2e-2 of the oracle's, ids as tests/helpers.py::assert_prefill_ids allows, decode steps fed the
+    oracle's ids with their logits within 2e-2."""
+    from helpers import assert_prefill_ids
+    from test_long_gpu import LOGIT_TOL, _forced_decode, _models
+
+    shape = dict(n_layer=2, dim=4096, n_head=32, ffn=11008, vocab=32000, ctx=320)
+    cfg, ref, model = _models(oracle, vk, ctx, shape, seed=31)
+    try:
+        prompt = oracle.prompt_tokens(32, 300, cfg.vocab)
+        offset = 0
+        for n in (100, 128, 72):
+            part = prompt[offset:offset + n]
+            print(f"[streamed chunks] rows {offset}..{offset + n - 1}", flush=True)
+            want_ids, want_logits, _ = ref.step(part, offset, want_logits=True)
+            ids = model.step(part, offset)
+            logits = model.last_logits(n)
+            err = float(np.max(np.abs(logits.astype(np.float32) - want_logits.astype(np.float32))))
+            print(f"[streamed chunks] max|dlogit| {err:.3g}")
+            assert err <= LOGIT_TOL
+            assert_prefill_ids(ids, want_ids, want_logits, f"{n}-row chunk at {offset}")
+            offset += n
+        # every decode step's logits within the tolerance; an id may differ only at a one-ulp tie (fp32 summation
+        # order decides those), at most one of the four steps
+        worst, ties = _forced_decode(ref, model, want_ids[-1], offset, 4)
+        print(f"[streamed chunks] decode max|dlogit| {worst:.3g}, {ties} one-ulp ties")
+        assert ties <= 1
+    finally:
+        ref.close()
+        model.close()
