@@ -54,7 +54,7 @@ struct FusedState
     // prompt steps of at most 128 tokens (VKLLM_PREFILL_TILED=0: off): fragment-tiled copies of the QKV, output,
     // gate/up and vocabulary matrices (one slab), streamed by launch_stream_gemm, and the fragment-ordered
     // activations it reads ([128, D] each: the normalised rows and the attention output)
-    bool stream_ok = false;
+    bool stream_ok = false, stream_tried = false;
     void *tile_slab = nullptr;
     struct Tiles
     {
@@ -177,6 +177,19 @@ void fused_plan_free(void *plan)
     delete (FusedPlan *)plan;
 }
 
+static void free_stream_tiles(FusedState *fs)
+{
+    void *bufs[] = {fs->tile_slab, fs->xn_t, fs->attn_t};
+    for (void *b : bufs)
+        if (b)
+            (void)hipFree(b);
+    fs->tile_slab = nullptr;
+    fs->xn_t = fs->attn_t = nullptr;
+    fs->out_t = nullptr;
+    fs->tiles.clear();
+    fs->stream_ok = false;
+}
+
 static void free_buffers(FusedState *fs)
 {
     void *bufs[] = {fs->h, fs->xn, fs->qkv, fs->q, fs->attn, fs->act, fs->ug, fs->logits, fs->ids, fs->toks,
@@ -221,8 +234,9 @@ void fused_model_release(vkllm_context *ctx, vkllm_models_llama2 *model)
         (void)hipFree(fs->step);
     if (fs->freqs)
         (void)hipFree(fs->freqs);
+    free_stream_tiles(fs);
     void *att[] = {fs->att_scores, fs->att_stats, fs->att_part, fs->att_count, fs->attn_sync, fs->att_long_sync,
-                   fs->gemm_work,  fs->tile_slab, fs->xn_t,      fs->attn_t};
+                   fs->gemm_work};
     for (void *b : att)
         if (b)
             (void)hipFree(b);
@@ -236,12 +250,14 @@ void fused_model_release(vkllm_context *ctx, vkllm_models_llama2 *model)
     mp->fs = nullptr;
 }
 
-// The fragment-tiled weight copies of the short-prompt products, made once from the slab. Shapes the streamed
-// products and their producers cannot take, or too little free memory, leave stream_ok false (those steps then run
-// on the row-major slab).
+// The fragment-tiled weight copies of the short-prompt products, made from the slab at the first prompt step of at
+// most 128 tokens (decode-only use never pays for them). Shapes the streamed products and their producers cannot
+// take, too little free memory, or a failed allocation leave stream_ok false: those steps then run on the row-major
+// slab.
 static vkllm_err_t build_stream_tiles(vkllm_context *ctx, ModelPriv *mp)
 {
     FusedState *fs = mp->fs;
+    fs->stream_tried = true;
     const char *e = getenv("VKLLM_PREFILL_TILED");
     if (e && *e == '0')
         return VKLLM_ERR_OK;
@@ -261,9 +277,15 @@ static vkllm_err_t build_stream_tiles(vkllm_context *ctx, ModelPriv *mp)
         return VKLLM_ERR_OK;
     }
     hipStream_t st = ctx->device->stream;
-    HIP_TRY(hipMalloc(&fs->tile_slab, total * 2));
-    HIP_TRY(hipMalloc(&fs->xn_t, (size_t)128 * D * 2));
-    HIP_TRY(hipMalloc(&fs->attn_t, (size_t)128 * D * 2));
+    if (hipMalloc(&fs->tile_slab, total * 2) != hipSuccess || hipMalloc(&fs->xn_t, (size_t)128 * D * 2) != hipSuccess ||
+        hipMalloc(&fs->attn_t, (size_t)128 * D * 2) != hipSuccess)
+    {
+        (void)hipGetLastError();
+        free_stream_tiles(fs);
+        log_error("short-prompt tiled weights: allocation of %.1f GB failed: prompt steps run on the row-major weights",
+                  total * 2 / 1e9);
+        return VKLLM_ERR_OK;
+    }
     // rows past a step's tokens are read (their outputs are dropped): keep them finite
     HIP_TRY(hipMemsetAsync(fs->xn_t, 0, (size_t)128 * D * 2, st));
     HIP_TRY(hipMemsetAsync(fs->attn_t, 0, (size_t)128 * D * 2, st));
@@ -347,8 +369,9 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         HIP_TRY(hipMemset(fs->att_long_sync, 0, H * vk::kAttnLongStride * sizeof(uint32_t)));
         HIP_TRY(hipMalloc(&fs->gemm_work, kGemmWorkElems * sizeof(float)));
         make_node_records(fs, mp->L);
-        _CHECK(build_stream_tiles(ctx, mp));
     }
+    if (S > 1 && S <= 128 && !mp->fs->stream_tried)
+        _CHECK(build_stream_tiles(ctx, mp));
     FusedState *fs = mp->fs;
     if (S <= fs->cap_S)
         return VKLLM_ERR_OK;
