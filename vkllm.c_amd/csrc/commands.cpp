@@ -9,6 +9,7 @@
 
 extern "C" vkllm_err_t vkllm_commands_new(struct vkllm_context *context, struct vkllm_commands **commands)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && commands);
     auto *c = (vkllm_commands *)calloc(1, sizeof(vkllm_commands));
     if (!c)
@@ -28,6 +29,7 @@ extern "C" vkllm_err_t vkllm_commands_new(struct vkllm_context *context, struct 
 
 extern "C" void vkllm_commands_free(struct vkllm_context *context, struct vkllm_commands *commands)
 {
+    DeviceScope device_scope(context);
     if (!commands)
         return;
     vkllm_array_commands_task_free(commands->defer_tasks);
@@ -37,6 +39,7 @@ extern "C" void vkllm_commands_free(struct vkllm_context *context, struct vkllm_
 
 extern "C" vkllm_err_t vkllm_commands_begin(struct vkllm_context *context, struct vkllm_commands *commands)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && commands);
     commands->recording = true;
     return VKLLM_ERR_OK;
@@ -44,6 +47,7 @@ extern "C" vkllm_err_t vkllm_commands_begin(struct vkllm_context *context, struc
 
 extern "C" vkllm_err_t vkllm_commands_end(struct vkllm_context *context, struct vkllm_commands *commands)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && commands);
     commands->recording = false;
     return VKLLM_ERR_OK;
@@ -65,6 +69,7 @@ void commands_note_write(vkllm_commands *cmds, vkllm_tensor *t)
 extern "C" vkllm_err_t vkllm_commands_upload(struct vkllm_context *context, struct vkllm_commands *commands,
                                              struct vkllm_tensor *tensor, const uint8_t *data, size_t bytes)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && commands && tensor && data);
     _CHECK_ARGS(bytes <= tensor->bytes);
     vkllm_tensor *b = tensor_base(tensor);
@@ -86,6 +91,7 @@ extern "C" vkllm_err_t vkllm_commands_upload(struct vkllm_context *context, stru
 extern "C" vkllm_err_t vkllm_commands_download(struct vkllm_context *context, struct vkllm_commands *commands,
                                                struct vkllm_tensor *tensor, uint8_t *data, size_t bytes)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && commands && tensor && data);
     _CHECK_ARGS(bytes <= tensor->bytes);
     vkllm_tensor *b = tensor_base(tensor);
@@ -113,6 +119,7 @@ extern "C" vkllm_err_t vkllm_commands_download(struct vkllm_context *context, st
 extern "C" void vkllm_commands_sync_tensor(struct vkllm_context *context, struct vkllm_commands *commands,
                                            struct vkllm_tensor *tensor, uint32_t dst_access, uint32_t dst_stage)
 {
+    DeviceScope device_scope(context);
     __UNUSED(context);
     __UNUSED(commands);
     __UNUSED(tensor);
@@ -122,6 +129,7 @@ extern "C" void vkllm_commands_sync_tensor(struct vkllm_context *context, struct
 
 extern "C" vkllm_err_t vkllm_commands_submit(struct vkllm_context *context, struct vkllm_commands *commands)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && commands);
     HIP_TRY(hipGetLastError());
     return VKLLM_ERR_OK;
@@ -129,6 +137,7 @@ extern "C" vkllm_err_t vkllm_commands_submit(struct vkllm_context *context, stru
 
 extern "C" vkllm_err_t vkllm_commands_wait_exec(struct vkllm_context *context, struct vkllm_commands *commands)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && commands);
     hipStream_t st = context->device->stream;
     for (size_t i = 0; i < commands->written_mapped->used_n; ++i)

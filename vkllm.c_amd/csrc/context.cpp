@@ -291,6 +291,7 @@ hipError_t timing_flush(vkllm_context *ctx)
 extern "C" vkllm_err_t vkllm_pipeline_query_exec_time(struct vkllm_context *context, struct vkllm_pipeline *pipeline,
                                                       uint64_t *cost)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && pipeline && cost);
     _CHECK_ARGS(context->device->timing);
     HIP_TRY(timing_flush(context));
@@ -320,6 +321,7 @@ extern "C" vkllm_err_t vkllm_hip_kernel_stats(struct vkllm_context *context, int
 
 extern "C" vkllm_err_t vkllm_hip_reset_kernel_stats(struct vkllm_context *context)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context);
     HIP_TRY(timing_flush(context));
     for (int i = 0; i < KID_COUNT; ++i)
@@ -405,6 +407,7 @@ extern "C" vkllm_err_t vkllm_context_new(uint32_t dev, struct vkllm_context **co
 
 extern "C" void vkllm_context_free(struct vkllm_context *ctx)
 {
+    DeviceScope device_scope(ctx);
     if (!ctx)
         return;
     if (ctx->device)
@@ -439,6 +442,7 @@ extern "C" vkllm_err_t vkllm_hip_set_exec_mode(struct vkllm_context *ctx, int mo
 
 extern "C" int vkllm_hip_get_exec_mode(struct vkllm_context *ctx)
 {
+    DeviceScope device_scope(ctx);
     return ctx ? ctx->device->exec_mode : -1;
 }
 
@@ -458,6 +462,7 @@ extern "C" vkllm_err_t vkllm_hip_set_timing(struct vkllm_context *ctx, int enabl
 
 extern "C" vkllm_err_t vkllm_hip_synchronize(struct vkllm_context *ctx)
 {
+    DeviceScope device_scope(ctx);
     _CHECK_ARGS(ctx);
     HIP_TRY(hipStreamSynchronize(ctx->device->stream));
     HIP_TRY(timing_flush(ctx));
@@ -466,6 +471,7 @@ extern "C" vkllm_err_t vkllm_hip_synchronize(struct vkllm_context *ctx)
 
 extern "C" const char *vkllm_hip_device_arch(struct vkllm_context *ctx)
 {
+    DeviceScope device_scope(ctx);
     return ctx ? ctx->device->props.gcnArchName : "";
 }
 

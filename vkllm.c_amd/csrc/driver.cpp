@@ -17,6 +17,7 @@ extern "C" vkllm_err_t vkllm_hip_token_loop(struct vkllm_context *context, struc
                                             const uint32_t *prompt, uint32_t prompt_len, uint32_t offset0,
                                             uint32_t n_steps, uint32_t *ids, uint64_t *step_ns, uint64_t *phase_ns)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && model && prompt && prompt_len > 0 && ids);
     if (phase_ns)
         memset(phase_ns, 0, 4 * sizeof(uint64_t));

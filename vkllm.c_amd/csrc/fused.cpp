@@ -900,6 +900,7 @@ vkllm_err_t fused_plan_run(vkllm_context *ctx, vkllm_graph *graph)
 extern "C" vkllm_err_t vkllm_hip_model_last_logits(struct vkllm_context *ctx, struct vkllm_models_llama2 *model,
                                                    uint16_t *dst, uint32_t rows)
 {
+    DeviceScope device_scope(ctx);
     _CHECK_ARGS(ctx && model && dst);
     ModelPriv *mp = model_priv(model);
     _CHECK_ARGS(mp && mp->fs && mp->fs->logits && rows <= mp->fs->cap_S);
@@ -912,6 +913,7 @@ extern "C" vkllm_err_t vkllm_hip_model_last_logits(struct vkllm_context *ctx, st
 extern "C" vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *ctx, struct vkllm_models_llama2 *model,
                                                    const char *family, uint32_t reps, uint64_t *total_ns)
 {
+    DeviceScope device_scope(ctx);
     _CHECK_ARGS(ctx && model && family && reps > 0 && total_ns);
     ModelPriv *mp = model_priv(model);
     _CHECK_ARGS(mp && mp->fs && mp->fs->cap_S >= 1 && mp->fs->h);
@@ -989,6 +991,7 @@ extern "C" vkllm_err_t vkllm_hip_gemm_streamed(struct vkllm_context *ctx, int ep
                                                const uint16_t *B, uint16_t *C, uint32_t M, uint32_t N, uint32_t K,
                                                uint32_t ldc, uint32_t splits)
 {
+    DeviceScope device_scope(ctx);
     _CHECK_ARGS(ctx && A && B && C && M > 0 && M <= 128 && N > 0 && K >= 16 && K % 16 == 0 && splits <= 8);
     _CHECK_ARGS(epi == vk::GEMM_PLAIN || epi == vk::GEMM_RESID || epi == vk::GEMM_SWIGLU);
     _CHECK_ARGS(epi == vk::GEMM_PLAIN ? ldc >= N : (epi == vk::GEMM_RESID ? ldc == N && N % 32 == 0 : N % 32 == 0 && ldc >= N / 2));
@@ -1034,6 +1037,7 @@ extern "C" vkllm_err_t vkllm_hip_gemm(struct vkllm_context *ctx, int epi, const 
                                       uint16_t *C, uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split,
                                       float *work, uint64_t work_elems)
 {
+    DeviceScope device_scope(ctx);
     _CHECK_ARGS(ctx && A && B && C && M > 0 && N > 0 && K >= 8 && K % 8 == 0);
     _CHECK_ARGS(epi == vk::GEMM_PLAIN || epi == vk::GEMM_SILU_HI || epi == vk::GEMM_RESID || epi == vk::GEMM_SWIGLU);
     _CHECK_ARGS(epi == vk::GEMM_SWIGLU ? (K % 64 == 0 && N % 64 == 0 && split * 2 == N && ldc >= split && ldc % 8 == 0)

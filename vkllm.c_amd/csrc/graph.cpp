@@ -100,6 +100,7 @@ static bool use_fused(vkllm_context *ctx, vkllm_graph *g)
 
 extern "C" vkllm_err_t vkllm_graph_init(struct vkllm_context *context, struct vkllm_graph *graph)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && graph && graph->output_node && graph->commands);
     // a fused step runs none of the node kernels: its plan validates what the fused kernels need instead
     if (use_fused(context, graph))
@@ -110,6 +111,7 @@ extern "C" vkllm_err_t vkllm_graph_init(struct vkllm_context *context, struct vk
 
 extern "C" vkllm_err_t vkllm_graph_run(struct vkllm_context *context, struct vkllm_graph *graph)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && graph && graph->output_node && graph->commands);
     if (use_fused(context, graph))
         return fused_plan_run(context, graph);
@@ -124,6 +126,7 @@ extern "C" vkllm_err_t vkllm_graph_run(struct vkllm_context *context, struct vkl
 
 extern "C" vkllm_err_t vkllm_graph_post_run(struct vkllm_context *context, struct vkllm_graph *graph)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && graph && graph->output_node && graph->commands);
     // a fused step ran none of the node kernels, so there is no per-node post-run work
     if (use_fused(context, graph))
@@ -134,6 +137,7 @@ extern "C" vkllm_err_t vkllm_graph_post_run(struct vkllm_context *context, struc
 
 extern "C" vkllm_err_t vkllm_graph_free(struct vkllm_context *context, struct vkllm_graph *graph)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && graph);
     // queued work may still read these tensors
     (void)hipStreamSynchronize(context->device->stream);

@@ -714,16 +714,8 @@ hipError_t launch_attn_long(hipStream_t st, const AttnDecodeArgs &a, int cu_coun
         (uint64_t)a.chunk * a.cmax < a.ctx || a.cmax > 256 || !a.part || !a.stats || !a.long_sync || !a.err)
         return hipErrorInvalidValue;
     const size_t lds = (size_t)a.chunk * sizeof(float);
-    static size_t cached_lds = 0;
-    static int per_cu = 0;
-    if (lds != cached_lds)
-    {
-        int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_long_kernel, 256, lds) != hipSuccess)
-            n = 0;
-        per_cu = n;
-        cached_lds = lds;
-    }
+    static uint64_t occ_memo = 0;
+    const int per_cu = std::max(occupancy_per_cu((const void *)attn_long_kernel, 256, lds, occ_memo), 0);
     // the blocks of a head wait for each other: all of them must be resident at once
     if ((uint64_t)a.H * a.cmax > (uint64_t)(cu_count > 0 ? cu_count : 256) * (uint32_t)per_cu)
         return hipErrorInvalidConfiguration;
@@ -771,17 +763,9 @@ template <int NV> static hipError_t launch_attn_o_nv(hipStream_t st, AttnOArgs a
 {
     const uint32_t D = a.at.H * a.at.hd;
     const size_t lds = std::max((size_t)kv_max * sizeof(float), (size_t)D * 2);
-    // resident blocks per CU at this LDS size, cached for the last size seen
-    static size_t cached_lds = 0;
-    static int per_cu = 0;
-    if (lds != cached_lds)
-    {
-        int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_o_kernel<NV>, kSmallThreads, lds) != hipSuccess)
-            n = 0;
-        per_cu = n;
-        cached_lds = lds;
-    }
+    // resident blocks per CU at this LDS size (0 when the query fails, which rejects the launch)
+    static uint64_t occ_memo = 0;
+    const int per_cu = std::max(occupancy_per_cu((const void *)attn_o_kernel<NV>, kSmallThreads, lds, occ_memo), 0);
     const uint32_t cap = (uint32_t)(cu_count > 0 ? cu_count : 256) * (uint32_t)per_cu;
     const uint32_t A = small_blocks(a.at), units = D / 2, NW = kSmallThreads / 64;
     if (cap <= A)

@@ -358,16 +358,11 @@ static hipError_t launch_pf_hd(hipStream_t st, dim3 grid, const uint16_t *q, con
                                uint16_t *out, uint32_t offset, uint32_t S, uint32_t H, uint32_t ctx, float scale,
                                bool xt)
 {
-    static bool attr_set = false; // LDS beyond the default 64 KB needs the attribute, once per kernel
+    static uint64_t attr_devs = 0; // devices on which the LDS limit is raised for this kernel
     constexpr size_t lds = pf_lds_bytes<HD>();
-    if (!attr_set)
-    {
-        hipError_t e = hipFuncSetAttribute((const void *)attn_prefill_mfma_kernel<HD>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess)
-            return e;
-        attr_set = true;
-    }
+    hipError_t e = lds_attr_once((const void *)attn_prefill_mfma_kernel<HD>, lds, attr_devs);
+    if (e != hipSuccess)
+        return e;
     attn_prefill_mfma_kernel<HD><<<grid, 256, lds, st>>>(q, kc, vc, out, offset, S, H, ctx, scale, xt);
     return hipGetLastError();
 }

@@ -11,6 +11,43 @@ namespace vk
 
 constexpr int kWave = 64;
 
+// Raises a kernel's dynamic LDS limit above the default 64 KB on the current device. The attribute is per device,
+// so `done` keeps one bit per device ordinal that has it (ordinals past 63 set it on every call).
+inline hipError_t lds_attr_once(const void *fn, size_t bytes, uint64_t &done)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess)
+        return e;
+    const uint64_t bit = dev >= 0 && dev < 64 ? 1ull << dev : 0;
+    if (bit && (__atomic_load_n(&done, __ATOMIC_ACQUIRE) & bit))
+        return hipSuccess;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e == hipSuccess && bit)
+        __atomic_fetch_or(&done, bit, __ATOMIC_RELEASE);
+    return e;
+}
+
+// Resident workgroups per CU of `fn` at `threads` threads and `lds` bytes of dynamic LDS on the current device, or -1
+// when the query fails. `memo` keeps the last answer in one word (LDS bytes in bits 32-63, device in 24-31, a valid
+// bit at 16, the count in 0-15), so callers on several threads or devices never pair a count with another size.
+inline int occupancy_per_cu(const void *fn, int threads, size_t lds, uint64_t &memo)
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess)
+        return -1;
+    const uint64_t key = ((uint64_t)(uint32_t)lds << 32) | ((uint64_t)(dev & 0xff) << 24) | (1ull << 16);
+    const uint64_t m = __atomic_load_n(&memo, __ATOMIC_ACQUIRE);
+    if (lds <= 0xffffffffu && (m & ~0xffffull) == key)
+        return (int)(m & 0xffff);
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, lds) != hipSuccess)
+        return -1;
+    if (lds <= 0xffffffffu && n >= 0 && n <= 0xffff)
+        __atomic_store_n(&memo, key | (uint64_t)n, __ATOMIC_RELEASE);
+    return n;
+}
+
 __device__ __forceinline__ float h2f(uint16_t h)
 {
     _Float16 v;

@@ -504,18 +504,10 @@ template <int EPI, int R, int NV> static hipError_t launch_fast(hipStream_t st, 
     const uint32_t units = gemv_units(EPI, a, R);
     if (units == 0 || (a.norm_w != nullptr) != gemv_normalises(EPI))
         return hipErrorInvalidValue;
-    // resident workgroups per CU at this kernel's register use and this K's LDS, cached for the last K seen
-    static size_t cached_lds = 0;
-    static int per_cu = 0;
+    // resident workgroups per CU at this kernel's register use and this K's LDS (at least 1: it only sizes the grid)
+    static uint64_t occ_memo = 0;
     const size_t lds = (size_t)a.K * 2;
-    if (lds != cached_lds)
-    {
-        int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_fast_kernel<EPI, R, NV>, 256, lds) != hipSuccess)
-            n = 1;
-        per_cu = n > 0 ? n : 1;
-        cached_lds = lds;
-    }
+    const int per_cu = std::max(occupancy_per_cu((const void *)gemv_fast_kernel<EPI, R, NV>, 256, lds, occ_memo), 1);
     // every wave gets the same number of units (the fewest that the resident waves can cover), so no wave runs an
     // extra unit while the others idle
     const uint32_t cap = (uint32_t)(cu_count > 0 ? cu_count : 256) * (uint32_t)per_cu;

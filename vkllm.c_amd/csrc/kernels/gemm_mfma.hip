@@ -669,16 +669,11 @@ static hipError_t launch_tile(hipStream_t st, const uint16_t *A, const uint16_t 
                               uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, uint32_t splits,
                               uint32_t kchunk)
 {
-    static bool attr_set = false; // LDS beyond the default 64 KB needs the attribute, once per kernel
+    static uint64_t attr_devs = 0; // devices on which the LDS limit is raised for this kernel
     const size_t lds = gemm_lds<BM, BN>();
-    if (!attr_set)
-    {
-        hipError_t e = hipFuncSetAttribute((const void *)gemm_kernel<BM, BN, EPI, SPLIT>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess)
-            return e;
-        attr_set = true;
-    }
+    hipError_t e = lds_attr_once((const void *)gemm_kernel<BM, BN, EPI, SPLIT>, lds, attr_devs);
+    if (e != hipSuccess)
+        return e;
     const uint32_t tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN, total = tm * tn;
     const uint32_t grid = (total + 7) / 8 * 8;
     gemm_kernel<BM, BN, EPI, SPLIT><<<dim3(grid, SPLIT ? splits : 1), 256, lds, st>>>(A, B, C, work, M, N, K, ldc,
@@ -691,16 +686,11 @@ static hipError_t launch_tile32(hipStream_t st, const uint16_t *A, const uint16_
                                 uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t split, uint32_t splits,
                                 uint32_t kchunk, uint32_t n_base = 0, const GemmRope *rope = nullptr)
 {
-    static bool attr_set = false;
+    static uint64_t attr_devs = 0; // devices on which the LDS limit is raised for this kernel
     const size_t lds = gemm_lds<BM, BN>();
-    if (!attr_set)
-    {
-        hipError_t e = hipFuncSetAttribute((const void *)gemm32_kernel<BM, BN, EPI, SPLIT, PF>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess)
-            return e;
-        attr_set = true;
-    }
+    hipError_t e = lds_attr_once((const void *)gemm32_kernel<BM, BN, EPI, SPLIT, PF>, lds, attr_devs);
+    if (e != hipSuccess)
+        return e;
     const uint32_t tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN, total = tm * tn;
     const uint32_t grid = (total + 7) / 8 * 8;
     gemm32_kernel<BM, BN, EPI, SPLIT, PF><<<dim3(grid, SPLIT ? splits : 1), 256, lds, st>>>(

@@ -38,6 +38,7 @@ extern "C" vkllm_err_t vkllm_hip_gemm_noalloc(struct vkllm_context *ctx, int epi
                                               const uint16_t *B, uint16_t *C, uint32_t M, uint32_t N, uint32_t K,
                                               uint32_t ldc, uint32_t split, uint64_t work_elems)
 {
+    DeviceScope device_scope(ctx);
     _CHECK_ARGS(ctx && A && B && C && M > 0 && N > 0 && K >= 8 && K % 8 == 0);
     _CHECK_ARGS(epi == vk::GEMM_PLAIN || epi == vk::GEMM_SILU_HI || epi == vk::GEMM_RESID || epi == vk::GEMM_SWIGLU);
     _CHECK_ARGS(epi == vk::GEMM_SWIGLU ? (K % 64 == 0 && N % 64 == 0 && split * 2 == N && ldc >= split && ldc % 8 == 0)

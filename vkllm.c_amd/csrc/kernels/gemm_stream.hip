@@ -281,16 +281,11 @@ template <int EPI, int MB, int CW>
 static hipError_t launch_stream_shape(hipStream_t st, const uint16_t *X, const uint16_t *Wt, uint16_t *C, float *work,
                                       uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t kchunk, dim3 grid)
 {
-    static bool attr_set = false; // LDS beyond the default 64 KB needs the attribute, once per kernel
+    static uint64_t attr_devs = 0; // devices on which the LDS limit is raised for this kernel
     constexpr size_t lds = (size_t)kStreamBufs * kStreamChunk * MB * 1024;
-    if (!attr_set)
-    {
-        hipError_t e = hipFuncSetAttribute((const void *)stream_gemm_kernel<EPI, MB, CW>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess)
-            return e;
-        attr_set = true;
-    }
+    hipError_t e = lds_attr_once((const void *)stream_gemm_kernel<EPI, MB, CW>, lds, attr_devs);
+    if (e != hipSuccess)
+        return e;
     stream_gemm_kernel<EPI, MB, CW><<<grid, (CW + 1) * 64, lds, st>>>(X, Wt, C, work, M, N, K, ldc, kchunk);
     return hipGetLastError();
 }

@@ -34,6 +34,7 @@ extern "C" vkllm_err_t vkllm_kvcache_new(struct vkllm_context *context, uint32_t
                                          uint32_t vcache_shape[4], uint32_t layer_counts,
                                          struct vkllm_kvcache **kvcache)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && kcache_shape && vcache_shape && kvcache);
     auto *p = (vkllm_kvcache *)calloc(1, sizeof(vkllm_kvcache));
     if (!p)
@@ -81,6 +82,7 @@ extern "C" vkllm_err_t vkllm_kvcache_update(struct vkllm_context *context, struc
                                             struct vkllm_tensor **key, struct vkllm_tensor **value, uint32_t layer,
                                             uint32_t offset)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && kvcache && key && value);
     vkllm_tensor *pk = *key, *pv = *value;
     _CHECK_ARGS(pk && pv);
@@ -110,6 +112,7 @@ extern "C" vkllm_err_t vkllm_kvcache_update(struct vkllm_context *context, struc
 
 extern "C" void vkllm_kvcache_free(struct vkllm_context *context, struct vkllm_kvcache *kvcache)
 {
+    DeviceScope device_scope(context);
     if (!kvcache)
         return;
     if (kvcache->kcaches)
@@ -493,6 +496,7 @@ static bool all_weights_present(const vkllm_models_llama2 *m, const char *file)
 extern "C" vkllm_err_t vkllm_models_llama2_load(struct vkllm_context *context, struct vkllm_models_llama2 *model,
                                                 const char *file)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && model && file);
     memset(model, 0, sizeof(*model));
     gguf::File f;
@@ -619,6 +623,7 @@ extern "C" vkllm_err_t vkllm_models_llama2_init_random(struct vkllm_context *con
                                                        struct vkllm_models_llama2 *model,
                                                        const struct vkllm_llama2_config *cfg, uint64_t seed)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && model && cfg);
     _CHECK_ARGS(cfg->block_count > 0 && cfg->embedding_length > 0 && cfg->head_count > 0 &&
                 cfg->feed_forward_length > 0 && cfg->vocab_size > 0 && cfg->context_length > 0);
@@ -691,6 +696,7 @@ extern "C" vkllm_err_t vkllm_models_llama2_init_random(struct vkllm_context *con
 
 extern "C" vkllm_err_t vkllm_models_llama2_free(struct vkllm_context *context, struct vkllm_models_llama2 *model)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && model);
     (void)hipStreamSynchronize(context->device->stream);
     if (model->meta.tokens)
@@ -763,6 +769,7 @@ extern "C" vkllm_err_t vkllm_llama2_build_ffn_layer(struct vkllm_context *contex
                                                     struct vkllm_tensor *input,
                                                     struct vkllm_llama2_ffn_layer_params params, uint32_t block_idx)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && graph && input && params.WD && params.WG && params.WU);
     const uint32_t batch = input->shapes[0], channel = input->shapes[1], seq = input->shapes[2];
     const uint32_t up_dim = params.WU->shapes[2];
@@ -841,6 +848,7 @@ extern "C" vkllm_err_t vkllm_llama2_build_self_attn_layer(struct vkllm_context *
                                                           struct vkllm_llama2_self_attn_layer_params params,
                                                           uint32_t block_idx)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && graph && input && params.WQ && params.WK && params.WV);
     vkllm_op_rope_params rope = {params.offsets, params.freq_base, false};
     const uint32_t hidden = params.WQ->shapes[3], nhd = params.WQ->shapes[2];
@@ -978,6 +986,7 @@ extern "C" vkllm_err_t vkllm_llama2_build_transformer_block(struct vkllm_context
                                                             struct vkllm_llama2_transformer_block_params params,
                                                             uint32_t block_idx)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && graph && input);
     _CHECK(vkllm_llama2_build_self_attn_layer(context, graph, kvcache, input, params.attn, block_idx));
     vkllm_tensor *attn_out = graph->nodes->data[graph->nodes->used_n - 1];
@@ -1052,6 +1061,7 @@ extern "C" vkllm_err_t vkllm_models_llama2_build_graph(struct vkllm_context *con
                                                        struct vkllm_tensor *input_toks, struct vkllm_graph *graph,
                                                        uint32_t offsets)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && model);
     _CHECK_ARGS(model->weights.tok_embed_weights && model->weights.output_norm_weight &&
                 model->weights.output_weight);

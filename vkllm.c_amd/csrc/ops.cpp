@@ -69,6 +69,7 @@ static bool view_in_bounds(const vkllm_tensor *t)
 extern "C" vkllm_err_t vkllm_op_copy_init(struct vkllm_context *context, struct vkllm_commands *commands,
                                           struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && commands && tensor);
     _CHECK_ARGS(tensor->srcs[0]);
     _CHECK_ARGS(tensor->op == VKLLM_OP_COPY);
@@ -86,6 +87,7 @@ extern "C" vkllm_err_t vkllm_op_copy_init(struct vkllm_context *context, struct 
 extern "C" vkllm_err_t vkllm_op_copy_run(struct vkllm_context *context, struct vkllm_commands *commands,
                                          struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK(vkllm_op_copy_init(context, commands, tensor));
     CHECK_VIEW(tensor->srcs[0]);
     CHECK_VIEW(tensor);
@@ -107,6 +109,7 @@ extern "C" vkllm_err_t vkllm_op_copy_post_run(struct vkllm_context *, struct vkl
 extern "C" vkllm_err_t vkllm_op_bin_init(struct vkllm_context *context, struct vkllm_commands *commands,
                                          struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && commands && tensor);
     _CHECK_ARGS(tensor->srcs[0] && tensor->srcs[1]);
     _CHECK_ARGS(tensor->op == VKLLM_OP_BIN);
@@ -127,6 +130,7 @@ extern "C" vkllm_err_t vkllm_op_bin_init(struct vkllm_context *context, struct v
 extern "C" vkllm_err_t vkllm_op_bin_run(struct vkllm_context *context, struct vkllm_commands *commands,
                                         struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK(vkllm_op_bin_init(context, commands, tensor));
     CHECK_VIEW(tensor->srcs[0]);
     CHECK_VIEW(tensor->srcs[1]);
@@ -152,6 +156,7 @@ extern "C" vkllm_err_t vkllm_op_bin_post_run(struct vkllm_context *, struct vkll
 extern "C" vkllm_err_t vkllm_op_embedding_init(struct vkllm_context *context, struct vkllm_commands *commands,
                                                struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && commands && tensor);
     _CHECK_ARGS(tensor->srcs[0] && tensor->srcs[1]);
     vkllm_tensor *idx = tensor->srcs[0], *table = tensor->srcs[1];
@@ -172,6 +177,7 @@ extern "C" vkllm_err_t vkllm_op_embedding_init(struct vkllm_context *context, st
 extern "C" vkllm_err_t vkllm_op_embedding_run(struct vkllm_context *context, struct vkllm_commands *commands,
                                               struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK(vkllm_op_embedding_init(context, commands, tensor));
     CHECK_VIEW(tensor->srcs[0]);
     CHECK_VIEW(tensor->srcs[1]);
@@ -199,6 +205,7 @@ extern "C" vkllm_err_t vkllm_op_embedding_post_run(struct vkllm_context *, struc
 extern "C" vkllm_err_t vkllm_op_rmsnorm_init(struct vkllm_context *context, struct vkllm_commands *commands,
                                              struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && commands && tensor);
     _CHECK_ARGS(tensor->srcs[0] && tensor->srcs[1]);
     _CHECK_ARGS(tensor->op == VKLLM_OP_RMSNORM);
@@ -215,6 +222,7 @@ extern "C" vkllm_err_t vkllm_op_rmsnorm_init(struct vkllm_context *context, stru
 extern "C" vkllm_err_t vkllm_op_rmsnorm_run(struct vkllm_context *context, struct vkllm_commands *commands,
                                             struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK(vkllm_op_rmsnorm_init(context, commands, tensor));
     CHECK_VIEW(tensor->srcs[0]);
     CHECK_VIEW(tensor->srcs[1]);
@@ -256,6 +264,7 @@ static bool is_mat_mul_vec(const vkllm_tensor *t)
 extern "C" vkllm_err_t vkllm_op_matmul_init(struct vkllm_context *context, struct vkllm_commands *commands,
                                             struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && commands && tensor);
     _CHECK_ARGS(tensor->srcs[0] && tensor->srcs[1]);
     _CHECK_ARGS(tensor->op == VKLLM_OP_MATMUL);
@@ -278,6 +287,7 @@ extern "C" vkllm_err_t vkllm_op_matmul_init(struct vkllm_context *context, struc
 extern "C" vkllm_err_t vkllm_op_matmul_run(struct vkllm_context *context, struct vkllm_commands *commands,
                                            struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK(vkllm_op_matmul_init(context, commands, tensor));
     vkllm_tensor *a = tensor->srcs[0], *b = tensor->srcs[1];
     const uint32_t M = tensor->shapes[2], N = tensor->shapes[3], K = a->shapes[3];
@@ -316,6 +326,7 @@ extern "C" vkllm_err_t vkllm_op_matmul_post_run(struct vkllm_context *, struct v
 extern "C" vkllm_err_t vkllm_op_rope_init(struct vkllm_context *context, struct vkllm_commands *commands,
                                           struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && commands && tensor);
     _CHECK_ARGS(tensor->srcs[0]);
     _CHECK_ARGS(tensor->op == VKLLM_OP_ROPE);
@@ -335,6 +346,7 @@ extern "C" vkllm_err_t vkllm_op_rope_init(struct vkllm_context *context, struct 
 extern "C" vkllm_err_t vkllm_op_rope_run(struct vkllm_context *context, struct vkllm_commands *commands,
                                          struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK(vkllm_op_rope_init(context, commands, tensor));
     CHECK_VIEW(tensor->srcs[0]);
     CHECK_VIEW(tensor);
@@ -362,6 +374,7 @@ extern "C" vkllm_err_t vkllm_op_rope_post_run(struct vkllm_context *, struct vkl
 extern "C" vkllm_err_t vkllm_op_softmax_init(struct vkllm_context *context, struct vkllm_commands *commands,
                                              struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && commands && tensor);
     _CHECK_ARGS(tensor->srcs[0]);
     _CHECK_ARGS(tensor->op == VKLLM_OP_SOFTMAX);
@@ -382,6 +395,7 @@ extern "C" vkllm_err_t vkllm_op_softmax_init(struct vkllm_context *context, stru
 extern "C" vkllm_err_t vkllm_op_softmax_run(struct vkllm_context *context, struct vkllm_commands *commands,
                                             struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK(vkllm_op_softmax_init(context, commands, tensor));
     CHECK_VIEW(tensor->srcs[0]);
     CHECK_VIEW(tensor);
@@ -406,6 +420,7 @@ extern "C" vkllm_err_t vkllm_op_softmax_post_run(struct vkllm_context *, struct 
 extern "C" vkllm_err_t vkllm_op_update_rows_init(struct vkllm_context *context, struct vkllm_commands *commands,
                                                  struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && commands && tensor);
     _CHECK_ARGS(tensor->srcs[0]);
     _CHECK_ARGS(tensor->op == VKLLM_OP_UPDATE_ROWS);
@@ -431,6 +446,7 @@ extern "C" vkllm_err_t vkllm_op_update_rows_init(struct vkllm_context *context, 
 extern "C" vkllm_err_t vkllm_op_update_rows_run(struct vkllm_context *context, struct vkllm_commands *commands,
                                                 struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK(vkllm_op_update_rows_init(context, commands, tensor));
     CHECK_VIEW(tensor->srcs[0]);
     CHECK_VIEW(tensor);
@@ -455,6 +471,7 @@ extern "C" vkllm_err_t vkllm_op_update_rows_post_run(struct vkllm_context *, str
 extern "C" vkllm_err_t vkllm_op_arg_max_init(struct vkllm_context *context, struct vkllm_commands *commands,
                                              struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && commands && tensor);
     _CHECK_ARGS(tensor->srcs[0]);
     _CHECK_ARGS(tensor->op == VKLLM_OP_ARG_MAX);
@@ -477,6 +494,7 @@ extern "C" vkllm_err_t vkllm_op_arg_max_init(struct vkllm_context *context, stru
 extern "C" vkllm_err_t vkllm_op_arg_max_run(struct vkllm_context *context, struct vkllm_commands *commands,
                                             struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK(vkllm_op_arg_max_init(context, commands, tensor));
     CHECK_VIEW(tensor->srcs[0]);
     CHECK_VIEW(tensor);
@@ -499,6 +517,7 @@ extern "C" vkllm_err_t vkllm_op_arg_max_post_run(struct vkllm_context *, struct 
 extern "C" vkllm_err_t vkllm_op_ffn_up_and_gate_init(struct vkllm_context *context, struct vkllm_commands *commands,
                                                      struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && commands && tensor);
     _CHECK_ARGS(tensor->srcs[0] && tensor->srcs[1] && tensor->srcs[2]);
     _CHECK_ARGS(tensor->op == VKLLM_OP_FFN_UP_AND_GATE);
@@ -523,6 +542,7 @@ extern "C" vkllm_err_t vkllm_op_ffn_up_and_gate_init(struct vkllm_context *conte
 extern "C" vkllm_err_t vkllm_op_ffn_up_and_gate_run(struct vkllm_context *context, struct vkllm_commands *commands,
                                                     struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK(vkllm_op_ffn_up_and_gate_init(context, commands, tensor));
     for (int i = 0; i < 3; ++i)
         CHECK_VIEW(tensor->srcs[i]);

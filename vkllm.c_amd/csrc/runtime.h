@@ -104,6 +104,28 @@ vkllm_err_t hip_fail(hipError_t e, const char *what, const char *file, int line)
             return hip_fail(_he, #_expr, __FILE__, __LINE__);                                                       \
     } while (0)
 
+// Makes the context's device current for one entry point and gives the caller's back on return. Allocations,
+// function attributes and occupancy queries act on the current device, and one thread may hold contexts on several
+// devices; the check is one hipGetDevice when the device is already current.
+struct DeviceScope
+{
+    int prev = -1;
+    explicit DeviceScope(const vkllm_context *ctx)
+    {
+        int cur = 0;
+        if (ctx && ctx->device && hipGetDevice(&cur) == hipSuccess && cur != ctx->device->device_id &&
+            hipSetDevice(ctx->device->device_id) == hipSuccess)
+            prev = cur;
+    }
+    ~DeviceScope()
+    {
+        if (prev >= 0)
+            (void)hipSetDevice(prev);
+    }
+    DeviceScope(const DeviceScope &) = delete;
+    DeviceScope &operator=(const DeviceScope &) = delete;
+};
+
 // ---- memory ----
 size_t pool_class(size_t bytes);
 void *pool_alloc(vkllm_gpu_device *dev, size_t bytes);

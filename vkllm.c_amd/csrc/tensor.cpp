@@ -116,6 +116,7 @@ extern "C" vkllm_err_t vkllm_tensor_new(struct vkllm_context *context, const cha
                                         const uint32_t n_srcs, const void *params, size_t params_bytes, bool mapped,
                                         struct vkllm_tensor **p)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && p);
     if (!shapes)
     {
@@ -185,6 +186,7 @@ extern "C" vkllm_err_t vkllm_tensor_new(struct vkllm_context *context, const cha
 
 extern "C" void vkllm_tensor_free(struct vkllm_context *context, struct vkllm_tensor *t)
 {
+    DeviceScope device_scope(context);
     if (!t)
         return;
     if (!t->data.is_ref)
@@ -200,6 +202,7 @@ extern "C" void vkllm_tensor_free(struct vkllm_context *context, struct vkllm_te
 
 extern "C" vkllm_err_t vkllm_tensor_flush_cache(struct vkllm_context *context, struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && tensor);
     if (!tensor->data.mapped)
     {
@@ -217,6 +220,7 @@ extern "C" vkllm_err_t vkllm_tensor_flush_cache(struct vkllm_context *context, s
 
 extern "C" vkllm_err_t vkllm_tensor_invalid_cache(struct vkllm_context *context, struct vkllm_tensor *tensor)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && tensor);
     if (!tensor->data.mapped)
     {
@@ -236,6 +240,7 @@ extern "C" vkllm_err_t vkllm_tensor_invalid_cache(struct vkllm_context *context,
 extern "C" vkllm_err_t vkllm_tensor_new_staging(struct vkllm_context *context, struct vkllm_tensor *tensor,
                                                 struct vkllm_tensor **staging)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && tensor && staging);
     return vkllm_tensor_new(context, "", tensor->shapes, tensor->dtype, VKLLM_OP_NONE, nullptr, 0, nullptr, 0, true,
                             staging);
@@ -271,6 +276,7 @@ extern "C" vkllm_err_t vkllm_tensor_permute(struct vkllm_context *context, struc
 extern "C" vkllm_err_t vkllm_tensor_copy_ref(struct vkllm_context *context, struct vkllm_tensor *tensor,
                                              struct vkllm_tensor **p)
 {
+    DeviceScope device_scope(context);
     _CHECK_ARGS(context && tensor && p);
     auto *t = node_alloc(context->device, 0);
     if (!t)
