@@ -247,7 +247,7 @@ def main():
     # device time per token: replays of the captured decode graph, back to back, no host work in between
     # (not available when graph replay is switched off, e.g. VKLLM_GRAPH=0 under a kernel tracer)
     replay_ns = None
-    if os.environ.get("VKLLM_GRAPH", "1") != "0":
+    if os.environ.get("VKLLM_GRAPH", "1") != "0" and args.timing_steps > 0:
         replay_ns = model.time_kernel("decode_step", args.timing_steps)
         log(f"decode graph replay: {replay_ns / 1e3:.1f} us per token = {1e9 / replay_ns:.1f} tok/s")
 

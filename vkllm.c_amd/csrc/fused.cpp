@@ -627,13 +627,15 @@ static vkllm_err_t enqueue_decode(vkllm_context *ctx, ModelPriv *mp, uint32_t va
 }
 
 // A short-prompt product streamed from its tiled weights; a STREAM_PARTIAL product then goes through the split-K
-// reduce with `reduce_epi` (GEMM_QKV_ROPE with `rope`, or GEMM_RESID into C with `norm`).
+// reduce with `reduce_epi` (GEMM_QKV_ROPE with `rope`, or GEMM_RESID into C with `norm`). STREAM_QKV_ROPE takes
+// `rope` itself.
 static hipError_t stream_product(hipStream_t st, FusedState *fs, int epi, const uint16_t *X, const uint16_t *Wt,
                                  uint16_t *C, uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, int reduce_epi = -1,
                                  const vk::GemmRope *rope = nullptr, const vk::GemmNorm *norm = nullptr)
 {
     uint32_t splits = 0;
-    hipError_t e = vk::launch_stream_gemm(st, epi, X, Wt, C, fs->gemm_work, kGemmWorkElems, M, N, K, ldc, &splits);
+    hipError_t e =
+        vk::launch_stream_gemm(st, epi, X, Wt, C, fs->gemm_work, kGemmWorkElems, M, N, K, ldc, &splits, rope);
     if (e != hipSuccess || epi != vk::STREAM_PARTIAL)
         return e;
     return vk::launch_gemm_reduce(st, reduce_epi, fs->gemm_work, C, M, N, splits, rope, norm);
@@ -672,7 +674,12 @@ static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S
         {
             const vk::GemmRope rope{fs->q, ly.kc, ly.vc, fs->rope_cs, offset, D, hd, mp->ctx};
             charge(ctx, fs, NS_Q, l);
-            KTRY(ctx, KID_F_GEMM, stream_product(st, fs, vk::STREAM_PARTIAL, xn, fs->tiles[l].wqkv, fs->qkv, S, 3 * D, D, 3 * D, vk::GEMM_QKV_ROPE, &rope));
+            // above 32 tokens the product splits the tokens and rotates in its own epilogue; shorter prompts split K
+            // and rotate in the reduce
+            if (S > 32)
+                KTRY(ctx, KID_F_GEMM, stream_product(st, fs, vk::STREAM_QKV_ROPE, xn, fs->tiles[l].wqkv, nullptr, S, 3 * D, D, 0, -1, &rope));
+            else
+                KTRY(ctx, KID_F_GEMM, stream_product(st, fs, vk::STREAM_PARTIAL, xn, fs->tiles[l].wqkv, fs->qkv, S, 3 * D, D, 3 * D, vk::GEMM_QKV_ROPE, &rope));
         }
         else if (rope_epi)
         {

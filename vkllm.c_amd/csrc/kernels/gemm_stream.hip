@@ -18,7 +18,9 @@
 // each); it writes a chunk two chunks ahead of the compute and requests the next one as it does, so its loads have
 // two chunks of compute to arrive. The waves meet at one barrier per chunk whose fences order only LDS, so the
 // weight loads stay in flight across it. Split K (STREAM_PARTIAL) gives products with few row blocks enough
-// workgroups; their fp32 partials go through the split-K reduce of gemm_mfma.hip.
+// workgroups; their fp32 partials go through the split-K reduce of gemm_mfma.hip. The QKV product splits the tokens
+// instead (two workgroups per row group, 64 tokens each, on one XCD one after the other, so the second reads the
+// weights from L2): no partials, and RoPE with the K/V append runs in its epilogue.
 #include <utility>
 
 #include "device_common.h"
@@ -111,17 +113,49 @@ hipError_t launch_tile_activations(hipStream_t st, const uint16_t *X, uint16_t *
     return hipGetLastError();
 }
 
-template <int EPI, int MB, int CW>
+// STREAM_QKV_ROPE: columns n .. n + 3 (n % 4 == 0) of token t, fp16-rounded as the split-K reduce rounds them: two
+// RoPE pairs of q or k rotated and stored, or four v values stored, as one 8-byte vector (rope_store8's arithmetic)
+__device__ __forceinline__ void rope_store4(const GemmRope &r, uint32_t t, uint32_t n, float a0, float a1, float a2,
+                                            float a3)
+{
+    const uint32_t region = (n >= r.D) + (n >= 2 * r.D), c = n - region * r.D, head = c / r.hd, dim = c % r.hd;
+    const float v0 = h2f(f2h(a0)), v1 = h2f(f2h(a1)), v2 = h2f(f2h(a2)), v3 = h2f(f2h(a3));
+    const size_t cache = ((size_t)head * r.ctx + r.offset + t) * r.hd + dim;
+    if (region == 2)
+    {
+        *(uint2 *)(r.vc + cache) = uint2{pack2(f2h(v0), f2h(v1)), pack2(f2h(v2), f2h(v3))};
+        return;
+    }
+    const float *cs = r.cs + ((size_t)t * (r.hd / 2) + dim / 2) * 2;
+    const uint2 o = {pack2(f2h(rope_mul_sub(cs[0], v0, cs[1], v1)), f2h(rope_mul_add(cs[1], v0, cs[0], v1))),
+                     pack2(f2h(rope_mul_sub(cs[2], v2, cs[3], v3)), f2h(rope_mul_add(cs[3], v2, cs[2], v3)))};
+    *(uint2 *)(region == 0 ? r.q + (size_t)t * r.D + c : r.kc + cache) = o;
+}
+
+// MS token parts: workgroup L takes row group g and token blocks [tb0, tb0 + MB). With MS > 1 the parts of a row
+// group get consecutive slots of one XCD (workgroups are dealt to the 8 XCDs round robin).
+template <int EPI, int MB, int CW, int MS>
 __global__ __launch_bounds__((CW + 1) * 64, 1) void stream_gemm_kernel(const uint16_t *__restrict__ X,
                                                                        const uint16_t *__restrict__ Wt, uint16_t *C,
                                                                        float *work, uint32_t M, uint32_t N,
-                                                                       uint32_t K, uint32_t ldc, uint32_t kchunk)
+                                                                       uint32_t K, uint32_t ldc, uint32_t kchunk,
+                                                                       GemmRope rope)
 {
     constexpr int U = kStreamAhead, KSC = kStreamChunk, NB = kStreamBufs;
     constexpr int BUFV = KSC * MB * 64; // 16-byte vectors per LDS buffer
     static_assert(U % KSC == 0, "the weight ring spans whole chunks");
     extern __shared__ u32x4 xs[];
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint32_t nrb = (N + 31) / 32;
+    uint32_t g = blockIdx.x, tb0 = 0;
+    if constexpr (MS > 1)
+    {
+        const uint32_t slot = blockIdx.x / 8;
+        g = (slot / MS) * 8 + blockIdx.x % 8;
+        tb0 = (slot % MS) * MB;
+        if (g * CW >= nrb)
+            return; // padding of the last XCD round (whole workgroup, before any barrier)
+    }
     const uint32_t kb = blockIdx.y * kchunk, ke = min(K, kb + kchunk);
     if (kb >= ke)
         return; // whole workgroup (the launcher sizes the splits so that none is empty)
@@ -140,7 +174,7 @@ __global__ __launch_bounds__((CW + 1) * 64, 1) void stream_gemm_kernel(const uin
                 const uint32_t ks = ks0 + min(c * KSC + j, nks - 1);
 #pragma unroll
                 for (int tb = 0; tb < MB; ++tb)
-                    r[j * MB + tb] = xp[(size_t)(ks * 4 + tb) * 64];
+                    r[j * MB + tb] = xp[(size_t)(ks * 4 + tb0 + tb) * 64];
             }
         };
         auto write = [&](uint32_t c) {
@@ -167,7 +201,7 @@ __global__ __launch_bounds__((CW + 1) * 64, 1) void stream_gemm_kernel(const uin
         return;
     }
 
-    const uint32_t nrb = (N + 31) / 32, rbw = blockIdx.x * CW + w, rb = min(rbw, nrb - 1);
+    const uint32_t rbw = g * CW + w, rb = min(rbw, nrb - 1);
     const u32x4 *wp = (const u32x4 *)Wt + ((size_t)rb * (K / 16) + ks0) * 64 + lane;
     f32x16 acc[MB];
 #pragma unroll
@@ -236,10 +270,17 @@ __global__ __launch_bounds__((CW + 1) * 64, 1) void stream_gemm_kernel(const uin
 #pragma unroll
     for (int tb = 0; tb < MB; ++tb)
     {
-        const uint32_t t = tb * 32 + lane % 32;
+        const uint32_t t = (tb0 + tb) * 32 + lane % 32;
         if (t >= M)
             continue;
-        if constexpr (EPI == STREAM_SWIGLU)
+        if constexpr (EPI == STREAM_QKV_ROPE)
+        {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                rope_store4(rope, t, rb * 32 + q * 8 + (lane / 32) * 4, acc[tb][q * 4], acc[tb][q * 4 + 1],
+                            acc[tb][q * 4 + 2], acc[tb][q * 4 + 3]);
+        }
+        else if constexpr (EPI == STREAM_SWIGLU)
         {
             // rows r < 8 are up rows u = (r / 4) * 8 + (lane / 32) * 4 + r % 4 of output block rb, r + 8 their gate
 #pragma unroll
@@ -277,16 +318,17 @@ __global__ __launch_bounds__((CW + 1) * 64, 1) void stream_gemm_kernel(const uin
     }
 }
 
-template <int EPI, int MB, int CW>
+template <int EPI, int MB, int CW, int MS = 1>
 static hipError_t launch_stream_shape(hipStream_t st, const uint16_t *X, const uint16_t *Wt, uint16_t *C, float *work,
-                                      uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t kchunk, dim3 grid)
+                                      uint32_t M, uint32_t N, uint32_t K, uint32_t ldc, uint32_t kchunk, dim3 grid,
+                                      const GemmRope &rope = GemmRope{})
 {
     static uint64_t attr_devs = 0; // devices on which the LDS limit is raised for this kernel
     constexpr size_t lds = (size_t)kStreamBufs * kStreamChunk * MB * 1024;
-    hipError_t e = lds_attr_once((const void *)stream_gemm_kernel<EPI, MB, CW>, lds, attr_devs);
+    hipError_t e = lds_attr_once((const void *)stream_gemm_kernel<EPI, MB, CW, MS>, lds, attr_devs);
     if (e != hipSuccess)
         return e;
-    stream_gemm_kernel<EPI, MB, CW><<<grid, (CW + 1) * 64, lds, st>>>(X, Wt, C, work, M, N, K, ldc, kchunk);
+    stream_gemm_kernel<EPI, MB, CW, MS><<<grid, (CW + 1) * 64, lds, st>>>(X, Wt, C, work, M, N, K, ldc, kchunk, rope);
     return hipGetLastError();
 }
 
@@ -307,12 +349,36 @@ static hipError_t launch_stream_mb(hipStream_t st, const uint16_t *X, const uint
     }
 }
 
+// [Wq; Wk; Wv] with RoPE: three compute waves per workgroup; above 32 tokens two token parts (256 workgroups at the
+// 7B widths: at 128 tokens the same time as two K ranges, with no partials to add)
+static hipError_t launch_stream_qkv(hipStream_t st, const uint16_t *X, const uint16_t *Wt, uint32_t M, uint32_t N,
+                                    uint32_t K, const GemmRope &r)
+{
+    if (!r.q || !r.kc || !r.vc || !r.cs || r.D == 0 || r.D % 32 != 0 || N != 3 * r.D || r.hd < 4 || r.hd % 4 != 0 ||
+        r.D % r.hd != 0 || r.offset + M > r.ctx)
+        return hipErrorInvalidValue;
+    const uint32_t groups = ((N + 31) / 32 + 2) / 3;
+    const dim3 split_grid((groups + 7) / 8 * 8 * 2, 1);
+    if (M > 64)
+        return launch_stream_shape<STREAM_QKV_ROPE, 2, 3, 2>(st, X, Wt, nullptr, nullptr, M, N, K, 0, K, split_grid, r);
+    if (M > 32)
+        return launch_stream_shape<STREAM_QKV_ROPE, 1, 3, 2>(st, X, Wt, nullptr, nullptr, M, N, K, 0, K, split_grid, r);
+    return launch_stream_shape<STREAM_QKV_ROPE, 1, 3>(st, X, Wt, nullptr, nullptr, M, N, K, 0, K, dim3(groups, 1), r);
+}
+
 hipError_t launch_stream_gemm(hipStream_t st, int epi, const uint16_t *X, const uint16_t *Wt, uint16_t *C,
                               float *work, size_t work_elems, uint32_t M, uint32_t N, uint32_t K, uint32_t ldc,
-                              uint32_t *splits)
+                              uint32_t *splits, const GemmRope *rope)
 {
     if (M == 0 || M > 128 || N == 0 || K == 0 || K % 16 != 0 || !splits)
         return hipErrorInvalidValue;
+    if (epi == STREAM_QKV_ROPE)
+    {
+        if (!rope)
+            return hipErrorInvalidValue;
+        *splits = 1;
+        return launch_stream_qkv(st, X, Wt, M, N, K, *rope);
+    }
     const uint32_t nrb = (N + 31) / 32, chunks = (K / 16 + kStreamChunk - 1) / kStreamChunk;
     // three compute waves for the SwiGLU product when that still fits one workgroup per CU (more CUs take part)
     const uint32_t cw = epi == STREAM_SWIGLU && (nrb + 2) / 3 <= 256 ? 3 : 4;

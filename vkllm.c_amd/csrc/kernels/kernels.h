@@ -219,6 +219,8 @@ enum StreamEpi : int
     STREAM_PARTIAL = 0, // work[z][M][N]: fp32 partials of K range z (N % 32 == 0), for launch_gemm_reduce
     STREAM_PLAIN = 1,   // C[m][n] = fp16(acc), row stride ldc
     STREAM_SWIGLU = 2,  // the interleaved [Wu; Wg] copy (N = 2F): C[m][f] = fp16(fp16(up) * fp16(silu(gate)))
+    STREAM_QKV_ROPE = 3, // [Wq; Wk; Wv] (N = 3 rope->D): q rotated into rope->q, k rotated and v into the caches, as
+                         // launch_gemm's GEMM_QKV_ROPE; C is not written
 };
 // halfs of the tiled copy of W [N, K] (F > 0: [Wu; Wg] with N = 2F, F % 16 == 0, rows interleaved in 16s)
 size_t stream_tiled_elems(uint32_t N, uint32_t K, uint32_t F);
@@ -226,10 +228,10 @@ hipError_t launch_tile_weights(hipStream_t st, const uint16_t *W, uint16_t *Wt, 
 // row-major X [M <= 128, K] -> fragment order (128 * K halfs, rows past M zero)
 hipError_t launch_tile_activations(hipStream_t st, const uint16_t *X, uint16_t *Xt, uint32_t M, uint32_t K);
 // *splits: K ranges wanted for STREAM_PARTIAL (0: enough for about one workgroup per CU); on return the ranges used
-// (1 for the other epilogues). work holds work_elems floats.
+// (1 for the other epilogues). work holds work_elems floats; rope is STREAM_QKV_ROPE's.
 hipError_t launch_stream_gemm(hipStream_t st, int epi, const uint16_t *X, const uint16_t *Wt, uint16_t *C,
                               float *work, size_t work_elems, uint32_t M, uint32_t N, uint32_t K, uint32_t ldc,
-                              uint32_t *splits);
+                              uint32_t *splits, const GemmRope *rope = nullptr);
 // The epilogue of split-K partials work[z][M][N] (z < splits, added in order), as launch_gemm applies it: GEMM_RESID
 // (C += the sum; with `norm`, the rows' RMSNorm as well) or GEMM_QKV_ROPE (`rope`'s q and caches).
 hipError_t launch_gemm_reduce(hipStream_t st, int epi, const float *work, uint16_t *C, uint32_t M, uint32_t N,

@@ -106,12 +106,16 @@ vkllm_err_t hip_fail(hipError_t e, const char *what, const char *file, int line)
 
 // Makes the context's device current for one entry point and gives the caller's back on return. Allocations,
 // function attributes and occupancy queries act on the current device, and one thread may hold contexts on several
-// devices; the check is one hipGetDevice when the device is already current.
+// devices. Only the outermost entry point of a call checks (one hipGetDevice when the device is already current):
+// the library's own calls into its entry points (a graph build creates hundreds of tensors) run on the same context.
+inline thread_local int tl_device_scope_depth = 0;
 struct DeviceScope
 {
     int prev = -1;
     explicit DeviceScope(const vkllm_context *ctx)
     {
+        if (tl_device_scope_depth++ > 0)
+            return;
         int cur = 0;
         if (ctx && ctx->device && hipGetDevice(&cur) == hipSuccess && cur != ctx->device->device_id &&
             hipSetDevice(ctx->device->device_id) == hipSuccess)
@@ -119,6 +123,7 @@ struct DeviceScope
     }
     ~DeviceScope()
     {
+        --tl_device_scope_depth;
         if (prev >= 0)
             (void)hipSetDevice(prev);
     }
