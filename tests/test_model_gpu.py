@@ -230,12 +230,13 @@ def test_qkv_rope_epilogue_matches_separate_kernel(ctx, vk, monkeypatch, prompt_
     assert np.array_equal(logits_a.view(np.uint16), logits_b.view(np.uint16))
 
 
-@pytest.mark.parametrize("prompt_len", [20, 100])
-def test_norm_in_split_k_reduce_matches_separate_pass(ctx, vk, monkeypatch, prompt_len):
+@pytest.mark.parametrize("prompt_len,dim", [(20, 4096), (100, 4096), (100, 5120)])
+def test_norm_in_split_k_reduce_matches_separate_pass(ctx, vk, monkeypatch, prompt_len, dim):
     """The residual add and the next RMSNorm in one pass over the split-K partials of Wo and Wd (prompts of at most
-    128 tokens split K) against the reduce followed by the separate RMSNorm, at the 7B widths: identical ids and
-    logits."""
-    shape = dict(n_layer=2, dim=4096, n_head=32, ffn=11008, vocab=32000, ctx=160)
+    128 tokens split K) against the reduce followed by the separate RMSNorm, at the 7B widths (one 16-byte vector
+    per thread) and the 13B widths (two for some threads): identical ids and logits."""
+    heads, ffn = {4096: (32, 11008), 5120: (40, 13824)}[dim]
+    shape = dict(n_layer=2, dim=dim, n_head=heads, ffn=ffn, vocab=32000, ctx=160)
     prompt = vk.prompt_tokens(10, prompt_len, shape["vocab"])
     # both arms on the tile GEMMs (the streamed short-prompt products need the fused norm and sum in another order)
     monkeypatch.setenv("VKLLM_PREFILL_TILED", "0")

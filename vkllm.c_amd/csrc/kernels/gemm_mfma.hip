@@ -659,6 +659,102 @@ __global__ __launch_bounds__(512) void gemm_resid_norm_kernel(const float *work,
         rmsnorm_row_to(C + (size_t)m * N, w, (u32x4 *)(y + (size_t)m * N), N, eps, red);
 }
 
+// gemm_resid_norm_kernel for rows of at most 512 VPT vectors: each thread keeps its vectors in registers from the
+// partial sums to the normalised output, and requests the residual and norm weights with the partials, so the row
+// makes one round trip to memory instead of three. The sums run in the same order (a thread's vectors ascending,
+// the same block_sum), so the outputs equal the generic kernel's bit for bit.
+template <int VPT>
+__global__ __launch_bounds__(512) void gemm_resid_norm_regs_kernel(const float *work, uint16_t *C, uint32_t M,
+                                                                   uint32_t N, uint32_t splits, const float *w,
+                                                                   uint16_t *y, float eps, bool xt)
+{
+    __shared__ float red[8];
+    const uint32_t m = blockIdx.x, nv = N / 8, tid = threadIdx.x;
+    const size_t total = (size_t)M * N;
+    u32x4 *cv = (u32x4 *)(C + (size_t)m * N);
+    const float4 *wv = (const float4 *)w;
+    // unconditional loads at clamped indices (a guarded load compiles to a branch and a wait per load)
+    u32x4 r[VPT];
+    float4 wa[VPT], wb[VPT];
+#pragma unroll
+    for (int j = 0; j < VPT; ++j)
+    {
+        const uint32_t i = min(tid + 512 * j, nv - 1);
+        r[j] = cv[i];
+        wa[j] = wv[2 * i];
+        wb[j] = wv[2 * i + 1];
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < VPT; ++j)
+    {
+        const uint32_t i = tid + 512 * j;
+        const uint32_t ic = min(i, nv - 1);
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+        for (uint32_t z = 0; z < splits; ++z)
+        {
+            const float4 *p = (const float4 *)(work + z * total + (size_t)m * N + 8 * ic);
+            const float4 a = p[0], b = p[1];
+            acc[0] += a.x;
+            acc[1] += a.y;
+            acc[2] += a.z;
+            acc[3] += a.w;
+            acc[4] += b.x;
+            acc[5] += b.y;
+            acc[6] += b.z;
+            acc[7] += b.w;
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            r[j][k] = pack2(f2h(half_lo(r[j][k]) + h2f(f2h(acc[2 * k]))),
+                            f2h(half_hi(r[j][k]) + h2f(f2h(acc[2 * k + 1]))));
+        if (i < nv)
+        {
+            cv[i] = r[j];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+            {
+                const float a = half_lo(r[j][k]), b = half_hi(r[j][k]);
+                ss += a * a;
+                ss += b * b;
+            }
+        }
+    }
+    ss = block_sum(ss, red);
+    const float alpha = 1.0f / sqrtf(ss / (float)N + eps);
+#pragma unroll
+    for (int j = 0; j < VPT; ++j)
+    {
+        const uint32_t i = tid + 512 * j;
+        if (i >= nv)
+            continue;
+        const float ws[8] = {wa[j].x, wa[j].y, wa[j].z, wa[j].w, wb[j].x, wb[j].y, wb[j].z, wb[j].w};
+        u32x4 o;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+        {
+            const float a = half_lo(r[j][k]), b = half_hi(r[j][k]);
+            o[k] = pack2(f2h((a * ws[2 * k]) * alpha), f2h((b * ws[2 * k + 1]) * alpha));
+        }
+        ((u32x4 *)y)[xt ? xt_vec(m, i) : (size_t)m * nv + i] = o;
+    }
+}
+
+// the residual-norm reduce for a row of N columns (one 512-thread workgroup per row)
+static hipError_t launch_resid_norm(hipStream_t st, const float *work, uint16_t *C, uint32_t M, uint32_t N,
+                                    uint32_t splits, const GemmNorm &norm)
+{
+    const uint32_t nv = N / 8;
+    if (nv <= 512)
+        gemm_resid_norm_regs_kernel<1><<<M, 512, 0, st>>>(work, C, M, N, splits, norm.w, norm.y, norm.eps, norm.xt);
+    else if (nv <= 1024)
+        gemm_resid_norm_regs_kernel<2><<<M, 512, 0, st>>>(work, C, M, N, splits, norm.w, norm.y, norm.eps, norm.xt);
+    else
+        gemm_resid_norm_kernel<<<M, 512, 0, st>>>(work, C, M, N, splits, norm.w, norm.y, norm.eps, norm.xt);
+    return hipGetLastError();
+}
+
 template <int BM, int BN> static size_t gemm_lds()
 {
     return (size_t)2 * (BM + BN) * kLdsRow * sizeof(uint16_t);
@@ -816,10 +912,8 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
                 if (e != hipSuccess)
                     return e;
                 // 512 threads a row (one 16-byte vector each at width 4096) keep a row's partial loads in flight
-                gemm_resid_norm_kernel<<<M, 512, 0, st>>>(work, C, M, N, splits, norm->w, norm->y, norm->eps,
-                                                          norm->xt);
                 *normed = true;
-                return hipGetLastError();
+                return launch_resid_norm(st, work, C, M, N, splits, *norm);
             }
         return launch_shape32<128, 128, EPI>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk, 0, rope);
     }
@@ -858,8 +952,7 @@ hipError_t launch_gemm_reduce(hipStream_t st, int epi, const float *work, uint16
             return launch_reduce<GEMM_RESID>(st, work, C, M, N, N, 0, splits, 0, nullptr);
         if (N % 8 != 0 || (norm->xt && (M > 128 || N % 16 != 0)))
             return hipErrorInvalidValue;
-        gemm_resid_norm_kernel<<<M, 512, 0, st>>>(work, C, M, N, splits, norm->w, norm->y, norm->eps, norm->xt);
-        return hipGetLastError();
+        return launch_resid_norm(st, work, C, M, N, splits, *norm);
     case GEMM_QKV_ROPE:
         if (!rope || N != 3 * rope->D)
             return hipErrorInvalidValue;
