@@ -63,7 +63,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
     constexpr int KS = HD / 32;           // 32-wide slices of the head dims (K of S^T = K . Q^T)
     constexpr int DB = HD / 16;           // 16-wide blocks of output dims
     constexpr int KROW = HD + 8;          // K tile row, halves (padded: the operand reads fall on distinct banks)
-    constexpr int VROW = kPfKeys + 8;     // V tile row ([dim][key]), halves
+    constexpr int VROW = kPfKeys + 8;     // V tile row ([dim][key]), halves (8-byte units swizzled, below)
     constexpr int KV = kPfKeys * HD / 8 / 256; // 16-byte K vectors per thread per block
     constexpr int VP = 32 * (HD / 8) / 256;    // (key pair, dim chunk) items per thread per block
     constexpr int VT = HD * (kPfKeys / 8) / 256; // transposed rule: (row, key chunk) vectors per thread
@@ -71,6 +71,9 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
     extern __shared__ __attribute__((aligned(16))) uint16_t pf_lds[];
     auto Kt = [&](int b) { return pf_lds + b * (kPfKeys * KROW); };
     auto Vt = [&](int b) { return pf_lds + 2 * kPfKeys * KROW + b * (HD * VROW); };
+    // The V tile is read as 8-byte units (4 keys) by 16 lanes of 16 consecutive rows, and rows 8 apart fall on the
+    // same banks (72-half rows); unit u of row r sits at u ^ ((r >> 3) & 1), so those 16 reads cover the 32 banks
+    // once. Every access below has a lane-constant swizzle bit, folded into a per-lane column offset.
 
     const uint32_t D = H * HD, h = blockIdx.y;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q4 = lane >> 4, c16 = lane & 15;
@@ -243,14 +246,15 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
 #pragma unroll
             for (int i = 0; i < VP; ++i)
             {
+                // rows 8 ch + 2 e (+ 1) swizzle by ch & 1 = (tid / 32) & 1 (256 i / 32 is even)
                 const uint32_t v = tid + 256 * i, p = v % 32, ch = v / 32;
+                const uint32_t col = (((p >> 1) ^ ((tid >> 5) & 1u)) << 2) + 2 * (p & 1);
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                 {
-                    *(uint32_t *)(Vt(buf) + (8 * ch + 2 * e) * VROW + 2 * p) =
-                        (va[SI][i][e] & 0xffffu) | (vb[SI][i][e] << 16);
-                    *(uint32_t *)(Vt(buf) + (8 * ch + 2 * e + 1) * VROW + 2 * p) =
-                        (va[SI][i][e] >> 16) | (vb[SI][i][e] & 0xffff0000u);
+                    uint16_t *row = Vt(buf) + (8 * ch + 2 * e) * VROW + col;
+                    *(uint32_t *)row = (va[SI][i][e] & 0xffffu) | (vb[SI][i][e] << 16);
+                    *(uint32_t *)(row + VROW) = (va[SI][i][e] >> 16) | (vb[SI][i][e] & 0xffff0000u);
                 }
             }
         }
@@ -260,10 +264,13 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
             for (int i = 0; i < VT; ++i)
             {
                 const uint32_t v = tid + 256 * i, n = v / (kPfKeys / 8), c = v % (kPfKeys / 8);
-                *(u32x4 *)(Vt(buf) + n * VROW + 8 * c) = vt[SI][i];
+                // units 2c and 2c + 1 trade places in the rows that swizzle ((n >> 3) & 1 = (tid >> 6) & 1)
+                const u32x4 x = vt[SI][i];
+                *(u32x4 *)(Vt(buf) + n * VROW + 8 * c) = ((tid >> 6) & 1u) ? u32x4{x[2], x[3], x[0], x[1]} : x;
             }
         }
     };
+    const uint32_t vcol = 4 * (q4 ^ ((c16 >> 3) & 1u));
     auto step2 = [&](auto ld, auto cur, auto nxt, int buf, uint32_t jb) {
         if constexpr (decltype(ld)::value >= 1)
         {
@@ -294,7 +301,8 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
 #pragma unroll
             for (int d = 0; d < DB; ++d)
             {
-                const uint16_t *vr = Vt(buf) + (16 * d + c16) * VROW + 32 * t + 4 * q4;
+                // row 16 d + c16 swizzles by (c16 >> 3) & 1: unit 8 t + q4 (+ 4) sits at 8 t + (q4 ^ that) (+ 4)
+                const uint16_t *vr = Vt(buf) + (16 * d + c16) * VROW + 32 * t + vcol;
                 const uint2 lo = *(const uint2 *)vr, hi = *(const uint2 *)(vr + 16);
                 f16x8a a;
                 const u32x4 w = {lo.x, lo.y, hi.x, hi.y};
