@@ -42,6 +42,14 @@ typedef float f32x4a __attribute__((ext_vector_type(4)));
 constexpr uint32_t kPfRows = 64; // query rows per workgroup
 constexpr uint32_t kPfKeys = 64; // positions per key block
 
+// K tile row pitch in halves. The score MFMA's A operand reads 16 rows x four 16-byte chunks per instruction; of the
+// pitches measured on gfx950 (LDS bank-conflict counter, that read pattern alone) only 72 dwords reads without
+// conflicts at head size 128; 68 and 76-132 take two passes.
+template <int HD> constexpr int pf_krow()
+{
+    return HD == 128 ? 144 : HD + 8;
+}
+
 // max / sum over the 4 lanes that hold one row (lanes l, l ^ 16, l ^ 32, l ^ 48)
 __device__ __forceinline__ float row4_max(float v)
 {
@@ -62,7 +70,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
 {
     constexpr int KS = HD / 32;           // 32-wide slices of the head dims (K of S^T = K . Q^T)
     constexpr int DB = HD / 16;           // 16-wide blocks of output dims
-    constexpr int KROW = HD + 8;          // K tile row, halves (padded: the operand reads fall on distinct banks)
+    constexpr int KROW = pf_krow<HD>();   // K tile row, halves (padded for the operand reads)
     constexpr int VROW = kPfKeys + 8;     // V tile row ([dim][key]), halves (8-byte units swizzled, below)
     constexpr int KV = kPfKeys * HD / 8 / 256; // 16-byte K vectors per thread per block
     constexpr int VP = 32 * (HD / 8) / 256;    // (key pair, dim chunk) items per thread per block
@@ -355,10 +363,10 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
     }
 }
 
-// LDS of the kernel: two K tiles [key][dim] and two V tiles [dim][key], rows padded by 8 halves
+// LDS of the kernel: two K tiles [key][dim] (pf_krow pitch) and two V tiles [dim][key] (rows padded by 8 halves)
 template <int HD> constexpr size_t pf_lds_bytes()
 {
-    return (size_t)2 * (kPfKeys * (HD + 8) + HD * (kPfKeys + 8)) * sizeof(uint16_t);
+    return (size_t)2 * (kPfKeys * pf_krow<HD>() + HD * (kPfKeys + 8)) * sizeof(uint16_t);
 }
 
 template <int HD>
