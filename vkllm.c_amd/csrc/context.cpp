@@ -360,6 +360,19 @@ extern "C" vkllm_err_t vkllm_context_new(uint32_t dev, struct vkllm_context **co
         log_error("device %u not found (%d visible)", dev, count);
         return VKLLM_ERR_DEV_NOT_FOUND;
     }
+    // the device is current while the context is set up; the caller's comes back on return, as after every entry
+    // point that takes the context
+    struct RestoreDevice
+    {
+        int d = -1;
+        ~RestoreDevice()
+        {
+            if (d >= 0)
+                (void)hipSetDevice(d);
+        }
+    } restore;
+    if (hipGetDevice(&restore.d) != hipSuccess)
+        restore.d = -1;
     HIP_TRY(hipSetDevice((int)dev));
     // the allocation-free GEMM's scratch array: its address on this device, looked up once with the device current
     {
@@ -422,6 +435,7 @@ extern "C" void vkllm_context_free(struct vkllm_context *ctx)
         node_pool_release(ctx->device);
         if (ctx->device->stream)
             (void)hipStreamDestroy(ctx->device->stream);
+        device_scope.release();
         delete ctx->device;
     }
     free(ctx->pipelines);

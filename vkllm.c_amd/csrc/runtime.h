@@ -78,6 +78,7 @@ struct vkllm_gpu_device
     std::vector<void *> pinned_all;
     // recycled tensor structs (a token step builds and frees one per graph node)
     std::vector<void *> node_free;
+    int scope_depth = 0; // entry points of this device's context on the call stack (DeviceScope)
     int exec_mode = VKLLM_EXEC_FUSED;
     int graph_replay = 1;
     int timing = 0;
@@ -107,23 +108,32 @@ vkllm_err_t hip_fail(hipError_t e, const char *what, const char *file, int line)
 // Makes the context's device current for one entry point and gives the caller's back on return. Allocations,
 // function attributes and occupancy queries act on the current device, and one thread may hold contexts on several
 // devices. Only the outermost entry point of a call checks (one hipGetDevice when the device is already current):
-// the library's own calls into its entry points (a graph build creates hundreds of tensors) run on the same context.
-inline thread_local int tl_device_scope_depth = 0;
+// the library's own calls into its entry points (a graph build creates hundreds of tensors) run on the same context,
+// whose nesting depth the device record keeps (a context is used by one thread at a time).
 struct DeviceScope
 {
-    int prev = -1;
+    vkllm_gpu_device *dev = nullptr; // the device record whose depth this scope counts
+    int prev = -1;                   // the caller's device, when this scope switched away from it
     explicit DeviceScope(const vkllm_context *ctx)
     {
-        if (tl_device_scope_depth++ > 0)
+        if (!ctx || !ctx->device)
+            return;
+        dev = ctx->device;
+        if (dev->scope_depth++ > 0)
             return;
         int cur = 0;
-        if (ctx && ctx->device && hipGetDevice(&cur) == hipSuccess && cur != ctx->device->device_id &&
-            hipSetDevice(ctx->device->device_id) == hipSuccess)
+        if (hipGetDevice(&cur) == hipSuccess && cur != dev->device_id && hipSetDevice(dev->device_id) == hipSuccess)
             prev = cur;
+    }
+    // before an entry point frees the device record: stop counting on it (the caller's device still comes back)
+    void release()
+    {
+        dev = nullptr;
     }
     ~DeviceScope()
     {
-        --tl_device_scope_depth;
+        if (dev)
+            --dev->scope_depth;
         if (prev >= 0)
             (void)hipSetDevice(prev);
     }
