@@ -27,7 +27,9 @@ CASES = [
     (1024, 22016, 1024, SILU_HI, 20000, True),  # SiLU split inside the tail columns
     (2048, 27648, 512, SILU_HI, 13824, True),   # 13B gate+up shape, 2048 tokens: three full rounds + tail
     (1200, 15300, 1024, RESID, 0, True),      # ragged M and N through the tail split, residual epilogue
-    (2048, 5120, 512, RESID, 0, True),        # 13B Wo shape: 160 tiles of 256 x 256 beat 2.5 rounds of 128 x 128
+    (2048, 5120, 512, RESID, 0, True),        # 13B Wo shape: 256 tiles of 128 x 320 instead of 160 of 256 x 256
+    (2000, 5000, 512, RESID, 0, True),        # the same rule, ragged M and N (partial 128 x 320 tiles)
+    (2048, 5120, 512, PLAIN, 0, True),        # plain epilogue: 160 tiles of 256 x 256 beat 2.5 rounds of 128 x 128
     (1100, 9000, 256, PLAIN, 0, True),        # the same rule, ragged M and N
     (128, 12288, 4096, PLAIN, 0, True),       # 128-token prompt: 128 x 128 tiles, split K, two K steps in flight
     (128, 12288, 4096, PLAIN, 0, False),      # the same without a work buffer: no split
@@ -48,9 +50,9 @@ CASES = [
     (100, 3072, 512, SWIGLU, 1536, False),    # ragged M, no work buffer
     # the LLaMA-2-13B prompt products at 2048 tokens with their real K (dim 5120, FFN 13824)
     (2048, 15360, 5120, PLAIN, 0, True),      # [Wq; Wk; Wv]
-    (2048, 5120, 5120, RESID, 0, True),       # Wo + residual: 160 tiles of 256 x 256
+    (2048, 5120, 5120, RESID, 0, True),       # Wo + residual: 256 tiles of 128 x 320
     (2048, 27648, 5120, SWIGLU, 13824, True),  # [Wu; Wg] with SwiGLU: three full rounds and the split-K tail
-    (2048, 5120, 13824, RESID, 0, True),      # Wd + residual
+    (2048, 5120, 13824, RESID, 0, True),      # Wd + residual: 256 tiles of 128 x 320
     (2048, 32000, 5120, PLAIN, 0, True),      # logits
     (77, 1000, 256, PLAIN, 0, True),          # ragged, one partial tile row
     (77, 1000, 1000, PLAIN, 0, True),         # K % 64 != 0: 128 x 64 tiles

@@ -866,6 +866,17 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
         const uint64_t r256 = (t256 + cus - 1) / cus, r128 = (2 * t256 + cus - 1) / cus;
         if (t256 >= (cus * 3) / 4 || r128 * 2 > r256 * 3)
         {
+            // Residual products whose 256 x 256 tiles make one partial round: 128 x 320 tiles when they give at
+            // least 1.5 times as many CUs a tile in one round (13B Wo and down at 2048 tokens: 256 tiles for 256
+            // CUs instead of 160; Wo + Wd 528 -> 485 us per layer, outputs bit-identical, since every output adds its
+            // K terms in the same order in either tile). The same tiles were slower for the plain vocabulary product,
+            // and 128 x 384 tiles level for the 7B QKV product at 1024 tokens.
+            if constexpr (EPI == GEMM_RESID)
+            {
+                const uint64_t t320 = (uint64_t)((M + 127) / 128) * ((N + 319) / 320);
+                if (t256 < cus && t320 <= cus && t320 * 2 >= t256 * 3)
+                    return launch_tile32<128, 320, EPI, false, 1>(st, A, B, C, work, M, N, K, ldc, split, 1, K);
+            }
             // A last round of 256 x 256 tiles at most half full would leave most CUs idle for a whole tile's time:
             // its tile columns run as a product of their own with K split over those CUs (partials added in order
             // by the reduce), the full rounds as before.
