@@ -83,9 +83,11 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
     // same banks (72-half rows); unit u of row r sits at u ^ ((r >> 3) & 1), so those 16 reads cover the 32 banks
     // once. Every access below has a lane-constant swizzle bit, folded into a per-lane column offset.
 
-    const uint32_t D = H * HD, h = blockIdx.y;
+    const uint32_t D = H * HD, h = blockIdx.x;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, q4 = lane >> 4, c16 = lane & 15;
-    const uint32_t row0 = blockIdx.x * kPfRows;
+    // heads vary fastest and row blocks run last to first: the workgroups with the most causal work start first, and
+    // a head's workgroups are dealt to one XCD (blocks go to the 8 XCDs round robin) when H is a multiple of 8
+    const uint32_t row0 = (gridDim.y - 1 - blockIdx.y) * kPfRows;
     const uint32_t rowc = min(row0 + wave * 16 + c16, S - 1); // this lane's query row (rows past S: not stored)
     const uint32_t pos = offset + rowc;
     const uint32_t kv = offset + S;
@@ -394,7 +396,7 @@ hipError_t launch_attn_prefill_mfma(hipStream_t st, const uint16_t *q, const uin
 {
     if (S == 0 || offset + S > ctx || !attn_prefill_mfma_ok(hd) || (xt && S > 128))
         return hipErrorInvalidValue;
-    const dim3 grid((S + kPfRows - 1) / kPfRows, H);
+    const dim3 grid(H, (S + kPfRows - 1) / kPfRows);
     if (hd == 128)
         return launch_pf_hd<128>(st, grid, q, kc, vc, out, offset, S, H, ctx, scale, xt);
     return launch_pf_hd<64>(st, grid, q, kc, vc, out, offset, S, H, ctx, scale, xt);
