@@ -83,7 +83,9 @@ def decode_families(shape, kv):
     VKLLM_ATTN_O=1), or the long-cache attention (one launch, or scores + P.V under VKLLM_ATTN_LONG=0)."""
     env = os.environ.get
     small_max = int(env("VKLLM_ATTN_SMALL_MAX", str(ATTN_SMALL_MAX)))
-    fam = ["fused_embed", "fused_qkv_rope", "fused_gateup", "fused_down_resid", "fused_logits", "fused_argmax"]
+    fam = ["fused_embed", "fused_qkv_rope", "fused_gateup", "fused_down_resid", "fused_logits"]
+    if env("VKLLM_ARGMAX_EPI", "1") == "0":  # else the arg max runs in the vocabulary product's launch
+        fam.append("fused_argmax")
     if kv <= small_max:
         return fam + (["fused_attn_o"] if env("VKLLM_ATTN_O", "0") == "1" else ["fused_attn_small", "fused_o_resid"])
     if env("VKLLM_ATTN_LONG", "1") == "0":
@@ -96,7 +98,8 @@ def step_bytes(shape, kv):
     b = decode_bytes(shape, kv)
     per_layer = sum(b[k] for k in ("fused_qkv_rope", "fused_attn_scores", "fused_o_resid", "fused_gateup",
                                    "fused_down_resid"))
-    return per_layer * shape["n_layer"] + b["fused_embed"] + b["fused_logits"] + b["fused_argmax"]
+    argmax = b["fused_argmax"] if "fused_argmax" in decode_families(shape, kv) else 0
+    return per_layer * shape["n_layer"] + b["fused_embed"] + b["fused_logits"] + argmax
 
 
 def read_traffic(kernel, tag):

@@ -212,6 +212,44 @@ def test_attention_and_projection_in_one_launch(ctx, vk, monkeypatch):
     assert np.array_equal(logits_a.view(np.uint16), logits_b.view(np.uint16))
 
 
+def test_arg_max_in_the_vocabulary_product(ctx, vk, monkeypatch):
+    """A single-token step's arg max in the vocabulary product's epilogue (each workgroup publishes its best, the last
+    to finish reduces them) against the separate ARG_MAX kernel and the reference's tie rule
+    (src/shaders/vkllm_arg_max.comp:40-97), with exact ties spread over the vocabulary: the output weights are zero
+    except rows +u at 5, 37, 70, 12345, 31999 and -u at 3, 35, 99, 20000, 31998 (u = 0.01 in every column), so one of
+    the two sets holds the row's maximum five times; the rule then picks 70 or 20000, neither the smallest tied
+    index. Identical ids and logits on both paths."""
+    from helpers import argmax_tie_rule
+
+    shape = dict(n_layer=2, dim=4096, n_head=32, ffn=11008, vocab=32000, ctx=160)
+    prompt = vk.prompt_tokens(11, 20, shape["vocab"])
+    plus, minus = [5, 37, 70, 12345, 31999], [3, 35, 99, 20000, 31998]
+    w = np.zeros((shape["vocab"], shape["dim"]), np.float16)
+    w[plus] = 0.01
+    w[minus] = -0.01
+
+    def run(epi):
+        monkeypatch.setenv("VKLLM_ARGMAX_EPI", epi)
+        vcfg = vk.llama_config(shape["n_layer"], shape["dim"], shape["n_head"], shape["ffn"], shape["vocab"],
+                               shape["ctx"])
+        model = vk.Model(ctx, config=vcfg, seed=7)
+        try:
+            ctx.upload(model.m.weights.output_weight, w)
+            return model.token_loop(prompt, 6, want_logits=True)
+        finally:
+            model.close()
+
+    ids_a, logits_a = run("1")
+    ids_b, logits_b = run("0")
+    assert ids_a.tolist() == ids_b.tolist()
+    assert np.array_equal(logits_a.view(np.uint16), logits_b.view(np.uint16))
+    for step in range(1, 6):  # the decode steps (step 0 is the prompt's last row)
+        row = logits_a[step].astype(np.float32)
+        tied = np.nonzero(row == row.max())[0].tolist()
+        assert tied in (plus, minus), tied
+        assert int(ids_a[step]) == argmax_tie_rule(row) and int(ids_a[step]) in (70, 20000)
+
+
 @pytest.mark.parametrize("prompt_len", [100, 300, 1030])
 def test_qkv_rope_epilogue_matches_separate_kernel(ctx, vk, monkeypatch, prompt_len):
     """RoPE and the K/V append in the prompt step's QKV product epilogue against the stored product and the separate

@@ -71,15 +71,20 @@ def test_reference_driver_runs_the_oracle_token_stream(oracle, tiny_gguf):
 def test_reference_driver_node_time_cost_loop(tiny_gguf):
     """The driver built with _LOG_NODE_TIME_COST sums vkllm_pipeline_query_exec_time over the graph nodes that have a
     pipeline into context->stats (tests/vkllm_test_infer_gguf.c:205-225) and prints the per-node table at the end
-    (:288-313, in whole milliseconds). With VKLLM_TIMING=1 the fused nodes are in it; without timing none is."""
-    env = dict(os.environ, VKLLM_TIMING="1")
-    r = subprocess.run([DRIVER_BIN + "_timing", tiny_gguf, "8"], capture_output=True, text=True, timeout=120, env=env)
-    assert r.returncode == 1, r.stderr[-2000:]
-    nodes = set(re.findall(r"node (\S+) total cost", r.stderr))
-    print(f"[driver] {len(nodes)} nodes timed")
-    for name in ("embedded", "block.0.attn.Q", "block.5.attn.scores", "block.3.attn.final_output", "block.2.ffn.up",
-                 "block.4.ffn.down", "logits", "output"):
-        assert name in nodes, name
+    (:288-313, in whole milliseconds; it adds up the decode steps only). With VKLLM_TIMING=1 the fused nodes are in
+    it; without timing none is. A decode step's arg max runs in the vocabulary product's launch, charged to "logits";
+    with VKLLM_ARGMAX_EPI=0 it is a launch of its own, charged to "output"."""
+    for argmax_epi in ("1", "0"):
+        env = dict(os.environ, VKLLM_TIMING="1", VKLLM_ARGMAX_EPI=argmax_epi)
+        r = subprocess.run([DRIVER_BIN + "_timing", tiny_gguf, "8"], capture_output=True, text=True, timeout=120,
+                           env=env)
+        assert r.returncode == 1, r.stderr[-2000:]
+        nodes = set(re.findall(r"node (\S+) total cost", r.stderr))
+        print(f"[driver] VKLLM_ARGMAX_EPI={argmax_epi}: {len(nodes)} nodes timed")
+        for name in ("embedded", "block.0.attn.Q", "block.5.attn.scores", "block.3.attn.final_output",
+                     "block.2.ffn.up", "block.4.ffn.down", "logits"):
+            assert name in nodes, name
+        assert ("output" in nodes) == (argmax_epi == "0")
     r = subprocess.run([DRIVER_BIN + "_timing", tiny_gguf, "4"], capture_output=True, text=True, timeout=120,
                        env={k: v for k, v in os.environ.items() if k != "VKLLM_TIMING"})
     assert r.returncode == 1

@@ -51,6 +51,12 @@ struct FusedState
     uint32_t *attn_sync = nullptr; // counters and flags of the attention + projection launch, zero between launches
     uint32_t *att_long_sync = nullptr; // per-head counters of the one-kernel long-cache attention, zero between launches
     float *gemm_work = nullptr;    // split-K partial tiles of short-prompt prefill GEMMs
+    // a single-token step's arg max in the vocabulary product's epilogue (VKLLM_ARGMAX_EPI=0: a separate kernel):
+    // per-workgroup candidates and the arrival counter (zero between launches); cleared when the product's shape
+    // does not take that epilogue
+    bool argmax_epi = true;
+    float *am_val = nullptr;
+    uint32_t *am_idx = nullptr, *am_count = nullptr;
     // prompt steps of at most 128 tokens (VKLLM_PREFILL_TILED=0: off): fragment-tiled copies of the QKV, output,
     // gate/up and vocabulary matrices (one slab), streamed by launch_stream_gemm, and the fragment-ordered
     // activations it reads ([128, D] each: the normalised rows and the attention output)
@@ -154,6 +160,8 @@ static void charge(vkllm_context *ctx, FusedState *fs, int slot, uint32_t l = UI
 // split-K workspace of the prefill GEMMs: 64 MB of fp32 partial tiles (4 splits of a 128-row QKV product at
 // dim 5120 need 31 MB)
 static constexpr size_t kGemmWorkElems = (size_t)16 << 20;
+// workgroups of the vocabulary product with the arg-max epilogue, at most (one candidate each)
+static constexpr uint32_t kArgmaxCandidates = 4096;
 
 static uint64_t host_ns()
 {
@@ -236,7 +244,7 @@ void fused_model_release(vkllm_context *ctx, vkllm_models_llama2 *model)
         (void)hipFree(fs->freqs);
     free_stream_tiles(fs);
     void *att[] = {fs->att_scores, fs->att_stats, fs->att_part, fs->att_count, fs->attn_sync, fs->att_long_sync,
-                   fs->gemm_work};
+                   fs->gemm_work,  fs->am_val,    fs->am_idx,   fs->am_count};
     for (void *b : att)
         if (b)
             (void)hipFree(b);
@@ -368,6 +376,12 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         HIP_TRY(hipMalloc(&fs->att_long_sync, H * vk::kAttnLongStride * sizeof(uint32_t)));
         HIP_TRY(hipMemset(fs->att_long_sync, 0, H * vk::kAttnLongStride * sizeof(uint32_t)));
         HIP_TRY(hipMalloc(&fs->gemm_work, kGemmWorkElems * sizeof(float)));
+        const char *am = getenv("VKLLM_ARGMAX_EPI");
+        fs->argmax_epi = !(am && *am == '0');
+        HIP_TRY(hipMalloc(&fs->am_val, kArgmaxCandidates * sizeof(float)));
+        HIP_TRY(hipMalloc(&fs->am_idx, kArgmaxCandidates * sizeof(uint32_t)));
+        HIP_TRY(hipMalloc(&fs->am_count, sizeof(uint32_t)));
+        HIP_TRY(hipMemset(fs->am_count, 0, sizeof(uint32_t)));
         make_node_records(fs, mp->L);
     }
     if (S > 1 && S <= 128 && !mp->fs->stream_tried)
@@ -514,7 +528,16 @@ static hipError_t launch_decode_kernel(vkllm_context *ctx, ModelPriv *mp, Kernel
         g.rows = V;
         g.units = (V + 1) / 2;
         g.out = fs->logits;
-        return vk::launch_gemv(st, vk::EPI_PLAIN, g, cu);
+        if (!fs->argmax_epi)
+            return vk::launch_gemv(st, vk::EPI_PLAIN, g, cu);
+        // the logits and their arg max (what KID_F_ARGMAX computes) in one launch
+        g.am_ids = fs->ids;
+        g.am_io = fs->dio;
+        g.am_val = fs->am_val;
+        g.am_idx = fs->am_idx;
+        g.am_count = fs->am_count;
+        g.am_cap = kArgmaxCandidates;
+        return vk::launch_gemv(st, vk::EPI_ARGMAX, g, cu);
     case KID_F_ARGMAX:
         return vk::launch_argmax_rows(st, fs->logits, fs->ids, 1, V, fs->dio);
     default:
@@ -620,6 +643,18 @@ static vkllm_err_t enqueue_decode(vkllm_context *ctx, ModelPriv *mp, uint32_t va
         }
         DTRY(ctx, mp, KID_F_GATEUP, l);
         DTRY(ctx, mp, KID_F_DOWN_RESID, l);
+    }
+    if (mp->fs->argmax_epi)
+    {
+        charge_decode(ctx, mp->fs, KID_F_LOGITS, 0);
+        const hipError_t e =
+            timed(ctx, pipeline_of(ctx, KID_F_LOGITS), [&]() { return launch_decode_kernel(ctx, mp, KID_F_LOGITS, 0); });
+        if (e == hipSuccess)
+            return VKLLM_ERR_OK;
+        if (e != hipErrorInvalidValue)
+            return hip_fail(e, "logits + arg max", __FILE__, __LINE__);
+        // the vocabulary product's shape does not take the arg-max epilogue (nothing was launched): two kernels
+        mp->fs->argmax_epi = false;
     }
     DTRY(ctx, mp, KID_F_LOGITS, 0);
     DTRY(ctx, mp, KID_F_ARGMAX, 0);

@@ -275,7 +275,7 @@ template <int EPI, int R> __device__ __forceinline__ void gemv_epilogue(const Ge
                                                                         const uint32_t *rows, const float *acc,
                                                                         const float *fq, const float *rs)
 {
-    if (EPI == EPI_PLAIN)
+    if (EPI == EPI_PLAIN || EPI == EPI_ARGMAX)
     {
 #pragma unroll
         for (int k = 0; k < R; ++k)
@@ -338,6 +338,84 @@ template <int EPI, int R> __device__ __forceinline__ void gemv_epilogue(const Ge
 constexpr bool gemv_normalises(int epi)
 {
     return epi != EPI_RESID;
+}
+
+// EPI_ARGMAX after the workgroup's last unit: (bv, bi) is lane 0's best of its wave's rows. The workgroup's best goes
+// out as agent-scope stores (written through to the level every XCD reads) and, once they are complete, one arrival
+// is counted; the workgroup that arrives last reads every candidate back with agent-scope loads, reduces them (the
+// order is total, so the grouping does not matter) and clears the counter for the next launch.
+__device__ __forceinline__ void gemv_argmax_finish(const GemvArgs &a, float bv, uint32_t bi)
+{
+    __shared__ float cv[4];
+    __shared__ uint32_t ci[4];
+    __shared__ uint32_t last;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    if (lane == 0)
+    {
+        cv[wid] = bv;
+        ci[wid] = bi;
+    }
+    __syncthreads();
+    if (tid == 0)
+    {
+        float v = cv[0];
+        uint32_t i = ci[0];
+        for (int w = 1; w < 4; ++w)
+            if (am_before(cv[w], ci[w], v, i))
+            {
+                v = cv[w];
+                i = ci[w];
+            }
+        __hip_atomic_store(a.am_val + blockIdx.x, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.am_idx + blockIdx.x, i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        last = __hip_atomic_fetch_add(a.am_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last)
+        return;
+    float v = -INFINITY;
+    uint32_t i = 0xFFFFFFFFu;
+    for (uint32_t j = tid; j < gridDim.x; j += 256)
+    {
+        const float w = __hip_atomic_load(a.am_val + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t k = __hip_atomic_load(a.am_idx + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (am_before(w, k, v, i))
+        {
+            v = w;
+            i = k;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1)
+    {
+        const float w = __shfl_xor(v, o, kWave);
+        const uint32_t k = (uint32_t)__shfl_xor((int)i, o, kWave);
+        if (am_before(w, k, v, i))
+        {
+            v = w;
+            i = k;
+        }
+    }
+    if (lane == 0)
+    {
+        cv[wid] = v;
+        ci[wid] = i;
+    }
+    __syncthreads();
+    if (tid == 0)
+    {
+        for (int w = 1; w < 4; ++w)
+            if (am_before(cv[w], ci[w], v, i))
+            {
+                v = cv[w];
+                i = ci[w];
+            }
+        a.am_ids[0] = i;
+        if (a.am_io)
+            a.am_io->id = i;
+        __hip_atomic_store(a.am_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 template <int EPI, int R, int NV> __global__ __launch_bounds__(256) void gemv_fast_kernel(GemvArgs a, uint32_t units)
@@ -447,7 +525,9 @@ template <int EPI, int R, int NV> __global__ __launch_bounds__(256) void gemv_fa
     }
     __syncthreads();
 
-    // 4. units
+    // 4. units (EPI_ARGMAX: lane 0 keeps the best of the rows it stores)
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
     while (u < units)
     {
         float acc[R];
@@ -485,8 +565,23 @@ template <int EPI, int R, int NV> __global__ __launch_bounds__(256) void gemv_fa
         for (int k = 0; k < R; ++k)
             acc[k] = wave_sum_dpp(acc[k]);
         if (lane == 0)
+        {
             gemv_epilogue<EPI, R>(a, cur, cur_rows, acc, cur_fq, cur_rs);
+            if constexpr (EPI == EPI_ARGMAX)
+#pragma unroll
+                for (int k = 0; k < R; ++k)
+                {
+                    const float v = h2f(f2h(acc[k]));
+                    if (cur_rows[k] < a.rows && am_before(v, cur_rows[k], bv, bi))
+                    {
+                        bv = v;
+                        bi = cur_rows[k];
+                    }
+                }
+        }
     }
+    if constexpr (EPI == EPI_ARGMAX)
+        gemv_argmax_finish(a, bv, bi);
 }
 
 // units of R rows for `a`; 0 when R does not fit the epilogue's pairing
@@ -517,6 +612,8 @@ template <int EPI, int R, int NV> static hipError_t launch_fast(hipStream_t st, 
     const uint32_t cap = (uint32_t)(cu_count > 0 ? cu_count : 256) * resident;
     const uint32_t per_wave = (units + 4 * cap - 1) / (4 * cap);
     const uint32_t blocks = (units + 4 * per_wave - 1) / (4 * per_wave);
+    if (EPI == EPI_ARGMAX && (blocks > a.am_cap || !a.am_ids || !a.am_val || !a.am_idx || !a.am_count))
+        return hipErrorInvalidValue;
     gemv_fast_kernel<EPI, R, NV><<<blocks, 256, lds, st>>>(a, units);
     return hipGetLastError();
 }
@@ -569,6 +666,22 @@ template <int EPI> static hipError_t launch_epi(hipStream_t st, const GemvArgs &
         }
     return hipErrorInvalidValue;
 }
+// EPI_ARGMAX: one row per unit (the vocabulary product)
+static hipError_t launch_argmax_epi(hipStream_t st, const GemvArgs &a, int cu_count, int NV)
+{
+    constexpr int EPI = EPI_ARGMAX;
+    switch (NV)
+    {
+        GEMV_NV_CASE(1, 2);
+        GEMV_NV_CASE(1, 4);
+        GEMV_NV_CASE(1, 8);
+        GEMV_NV_CASE(1, 12);
+        GEMV_NV_CASE(1, 16);
+        GEMV_NV_CASE(1, 22);
+        GEMV_NV_CASE(1, 28);
+    }
+    return hipErrorInvalidValue;
+}
 #undef GEMV_NV_CASE
 
 // rows per unit: the number of 16-byte vectors each lane keeps in flight is R * NV
@@ -599,11 +712,13 @@ hipError_t launch_gemv(hipStream_t st, int epi, const GemvArgs &a, int cu_count)
             return launch_epi<EPI_GATEUP>(st, a, cu_count, R, NV);
         case EPI_QKV:
             return launch_epi<EPI_QKV>(st, a, cu_count, R, NV);
+        case EPI_ARGMAX:
+            return R == 1 ? launch_argmax_epi(st, a, cu_count, NV) : hipErrorInvalidValue;
         default:
             return hipErrorInvalidValue;
         }
     }
-    return launch_gemv_loop(st, epi, a, cu_count);
+    return epi == EPI_ARGMAX ? hipErrorInvalidValue : launch_gemv_loop(st, epi, a, cu_count);
 }
 
 // ---------------------------------------------------------------------------------------------------------------

@@ -73,6 +73,10 @@ enum GemvEpi : int
     EPI_RESID = 1, // out[r] = fp16(resid[r] + fp16(acc_r)), in place allowed
     EPI_GATEUP = 2, // rows [0,F) up, [F,2F) gate: out[r] = fp16(fp16(up_r) * fp16(silu(gate_r)))
     EPI_QKV = 3,   // rows [0,3D) of [Wq;Wk;Wv]: RoPE on q,k; q -> out, k/v -> caches at step->offset
+    // EPI_PLAIN's out, and the arg max of all rows under the reference's order (am_before) into am_ids[0] and
+    // am_io->id: each workgroup publishes its best (value, row), the last to arrive on am_count reduces them and
+    // clears the counter (no workgroup waits for another)
+    EPI_ARGMAX = 4,
 };
 
 struct GemvArgs
@@ -92,6 +96,13 @@ struct GemvArgs
     const Step *step;
     const float *freqs;     // base^(2w/hd), w < hd/2
     uint32_t D, hd, ctx;
+    // EPI_ARGMAX (fast kernel only, one row per unit; a launch of more than am_cap workgroups is refused)
+    uint32_t *am_ids;   // [1]
+    DecodeIo *am_io;    // optional
+    float *am_val;      // per-workgroup candidates [am_cap]
+    uint32_t *am_idx;   // [am_cap]
+    uint32_t *am_count; // arrivals, zero between launches
+    uint32_t am_cap;
 };
 hipError_t launch_gemv(hipStream_t st, int epi, const GemvArgs &a, int cu_count);
 
