@@ -5,10 +5,10 @@ The fused prompt step runs every matmul node of the reference graph (src/core/vk
 src/shaders/vkllm_matmul.comp) through this GEMM: C = A . B^T with fp16 operands and fp32 accumulation, rounded
 once to fp16, with the SiLU or residual epilogue fused. The model tests reach it only at the tiny workload's
 sizes; these cases reach the paths that 7B and 13B prompts take: 256 x 256 tiles, the split-K tail of a partial
-last round of those tiles, 128 x 128 tiles with and without split K, the 64-wide fallback tiles (K not a multiple
-of 64), ragged M and N, and the SwiGLU epilogue that reads [Wu; Wg] as interleaved row blocks. The bar is the
-fp16 rounding of an fp32 sum: |C - ref| <= 1e-3 + 2e-3 |ref|, twice that for the residual and SwiGLU epilogues,
-which round twice.
+last round of those tiles, one round of them with K split (residual products of long rows), 128 x 128 tiles with
+and without split K, the 64-wide fallback tiles (K not a multiple of 64), ragged M and N, and the SwiGLU epilogue
+that reads [Wu; Wg] as interleaved row blocks. The bar is the fp16 rounding of an fp32 sum:
+|C - ref| <= 1e-3 + 2e-3 |ref|, twice that for the residual and SwiGLU epilogues, which round twice.
 """
 import ctypes
 
@@ -54,6 +54,11 @@ CASES = [
     (2048, 27648, 5120, SWIGLU, 13824, True),  # [Wu; Wg] with SwiGLU: three full rounds and the split-K tail
     (2048, 5120, 13824, RESID, 0, True),      # Wd + residual: 256 tiles of 128 x 320
     (2048, 32000, 5120, PLAIN, 0, True),      # logits
+    # residual products with long rows whose 256 x 256 tiles leave CUs idle: K split over one round of them
+    (1024, 4096, 11008, RESID, 0, True),      # 7B Wd, 1024 tokens: 64 tiles x 4 K ranges
+    (1024, 5120, 5120, RESID, 0, True),       # 13B Wo, 1024 tokens: 80 tiles x 3
+    (640, 4096, 11008, RESID, 0, True),       # ragged last row tile: 48 tiles x 5
+    (1024, 4096, 4096, RESID, 0, True),       # 7B Wo (K 4096) stays on 128 x 128 tiles
     (77, 1000, 256, PLAIN, 0, True),          # ragged, one partial tile row
     (77, 1000, 1000, PLAIN, 0, True),         # K % 64 != 0: 128 x 64 tiles
     (300, 1000, 1000, SILU_HI, 500, True),    # K % 64 != 0, M > 128

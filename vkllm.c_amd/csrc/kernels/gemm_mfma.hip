@@ -902,6 +902,30 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
             }
             return launch_shape32<256, 256, EPI>(st, A, B, C, work, M, N, K, ldc, split, 1, K, 0, rope);
         }
+        // Residual products of long rows (K >= 5120: 13B Wo, 7B and 13B down) above 128 tokens whose 256 x 256 tiles
+        // leave most CUs idle: K split s ways so that one round of 256 x 256 tiles fills at least three quarters of
+        // the CUs, each split keeping at least 1280 of K. Against the 128 x 128 path: 7B down at 1024 tokens 110 vs
+        // 135 us (4 splits), 13B down 145 vs 250 us (3), 13B Wo 84 vs 108 us (3), 7B down at 640 tokens 92 vs 127 us
+        // (5), 7 to 30% at 384-2048 tokens; 7B Wo (K 4096) is level or slower at every length and stays on 128 x 128.
+        if constexpr (EPI == GEMM_RESID)
+        {
+            const uint32_t s = t256 > 0 ? (uint32_t)(cus / t256) : 0;
+            if (M > 128 && K >= 5120 && s >= 2 && t256 * s * 4 >= (uint64_t)cus * 3 && K / s >= 1280 &&
+                (size_t)s * M * N <= work_elems)
+            {
+                const uint32_t kchunk = ((K + s - 1) / s + kBK - 1) / kBK * kBK, ns = (K + kchunk - 1) / kchunk;
+                hipError_t e =
+                    launch_tile32<256, 256, EPI, true, 1>(st, A, B, C, work, M, N, K, ldc, split, ns, kchunk);
+                if (e != hipSuccess)
+                    return e;
+                if (norm)
+                {
+                    *normed = true;
+                    return launch_resid_norm(st, work, C, M, N, ns, *norm);
+                }
+                return launch_reduce<EPI>(st, work, C, M, N, ldc, split, ns, 0, nullptr);
+            }
+        }
         const uint64_t tiles = (uint64_t)((M + 127) / 128) * ((N + 127) / 128);
         // prompts of at most 128 tokens whose tiles cover two thirds of the CUs or more ([Wu;Wg], logits): the
         // whole K per tile with four K steps of loads in flight (one workgroup per CU) beats split K and its reduce
