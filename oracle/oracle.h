@@ -2,7 +2,7 @@
  * CPU oracle for the vkllm.c LLaMA-2 token loop.
  *
  * TEST INFRASTRUCTURE ONLY. Nothing in the shipped library links, loads or calls this code; only tests/,
- * __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, and only as the checker.
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, and only to check the library's results.
  *
  * It restates, in plain C, the semantics of the reference's operators and of its LLaMA-2 graph. Each function
  * cites the reference file:line it follows (paths relative to the vkllm.c tree).
@@ -110,7 +110,7 @@ int oracle_ffn_up_and_gate(const oracle_tensor *x, const oracle_tensor *wu, cons
 /* ---- REF16: the reference's fp16-arithmetic shader variants ----
  * With fp16 arithmetic on the device the reference selects the f16f16 variants (src/core/vkllm_op_matmul.c:92-101,
  * src/core/vkllm_op_rope.c:22, src/core/vkllm_op_softmax.c:24; macros at src/shaders/BUILD:81,101,120,140) instead
- * of the fp32-arithmetic ones this build follows. The residual adds and the up * gate product (bin_op f16f16f16,
+ * of the fp32-arithmetic ones the library follows. The residual adds and the up * gate product (bin_op f16f16f16,
  * src/shaders/BUILD:24) round one fp16 operation and RMSNorm has no fp16-arithmetic variant (BUILD:55-68), so those
  * are as in the fp32 mode. REF16
  * restates them: every arithmetic operation on fp16 values rounds its exact result once to fp16 (round to nearest

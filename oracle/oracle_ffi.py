@@ -1,7 +1,7 @@
 """ctypes access to the CPU oracle (oracle/build/liboracle.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, always as
-the checker. The shipped library never loads it.
+the side that the library's results are compared with. The shipped library never loads it.
 """
 import ctypes
 import os

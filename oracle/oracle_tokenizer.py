@@ -1,5 +1,5 @@
-"""CPU restatement of the reference's LLaMA-2 tokenizer. TEST INFRASTRUCTURE ONLY: imported by tests/ as the checker
-of vkllm_models_llama2_tokenize; the shipped library never loads it.
+"""CPU restatement of the reference's LLaMA-2 tokenizer. TEST INFRASTRUCTURE ONLY: imported by tests/ to check
+vkllm_models_llama2_tokenize; the shipped library never loads it.
 
 Follows vkllm_models_llama2_tokenize, src/models/vkllm_models_llama2.c:652-816, with its helpers
 find_token_by_text (:604-614) and find_best_merge (:616-650):

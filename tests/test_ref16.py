@@ -1,7 +1,7 @@
 """REF16: the oracle's restatement of the reference's fp16-arithmetic shader variants (src/shaders/BUILD:81,101,120,
 140; selected by src/core/vkllm_op_matmul.c:92-101, vkllm_op_rope.c:22 and vkllm_op_softmax.c:24 when the device has
 fp16 arithmetic), against values derived by hand from fp16 rounding, and the drift it measures between such a device
-and the fp32-arithmetic variants this build follows.
+and the fp32-arithmetic variants the library follows.
 
 Pins: the double -> fp16 rounding against numpy's own float64 -> float16 conversion; the GEMV's per-lane fp16
 accumulation by its stagnation point (adding 4 to 8192 is a tie that rounds back to 8192); its fp16 scale and SiLU by
