@@ -176,6 +176,35 @@ def test_7b_widths_two_layers(ctx, vk, oracle):
     assert ids.tolist() == want_ids.tolist()
 
 
+@pytest.mark.parametrize("dim,heads,ffn", [(4096, 32, 11008), (5120, 40, 13824)], ids=["7b", "13b"])
+def test_300_token_prompt_at_real_widths(ctx, vk, oracle, dim, heads, ffn):
+    """A 300-token prompt at the 7B and 13B widths (one layer, vocabulary 1000 to keep the oracle quick): the down
+    product (K 11008 / 13824) splits K 8 / 6 ways over one round of 256 x 256 tiles, and the reduce adds the residual
+    and the next RMSNorm. Every prompt row against the oracle (logits within 2e-2, ids identical but at one-ulp
+    ties), then 3 decode steps fed the oracle's ids (free-running streams part at the first one-ulp tie: with seed 13
+    the 13B widths have one at the first decode step, top-2 logits 0.0039 apart)."""
+    from test_long_gpu import _forced_decode
+
+    shape = dict(n_layer=1, dim=dim, n_head=heads, ffn=ffn, vocab=1000, ctx=320)
+    cfg = oracle.make_cfg(**shape)
+    ref = oracle.Model(cfg=cfg, seed=13)
+    model = vk.Model(ctx, config=vk.llama_config(1, dim, heads, ffn, 1000, 320), seed=13)
+    try:
+        prompt = oracle.prompt_tokens(14, 300, cfg.vocab)
+        want_ids, want_logits, _ = ref.step(prompt, 0, want_logits=True)
+        ids = model.step(prompt, 0)
+        err = float(np.max(np.abs(model.last_logits(300).astype(np.float32) - want_logits.astype(np.float32))))
+        print(f"[300-token prompt] max|dlogit| {err:.3g}")
+        assert err <= LOGIT_TOL
+        assert_prefill_ids(ids, want_ids, want_logits, "300-token prompt")
+        worst, ties = _forced_decode(ref, model, want_ids[-1], 300, 3)
+        print(f"[decode] max|dlogit| {worst:.3g}, {ties} one-ulp ties")
+        assert ties <= 1
+    finally:
+        ref.close()
+        model.close()
+
+
 @pytest.mark.parametrize("small_max,long_one", [("1536", "1"), ("512", "1"), ("512", "0")])
 def test_long_context_decode(ctx, vk, oracle, monkeypatch, small_max, long_one):
     """Decode at kv 1001..1008 (head_dim 128, a 1000-token prompt, 8 steps). With the one-kernel attention admitted
