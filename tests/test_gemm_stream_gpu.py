@@ -163,3 +163,31 @@ def test_streamed_prefill_in_chunks(ctx, vk, oracle):
     finally:
         ref.close()
         model.close()
+
+
+@pytest.mark.parametrize("prompt_len", [40, 100])
+def test_streamed_prefill_13b_widths(ctx, vk, oracle, prompt_len):
+    """Prompt steps at the 13B widths (dim 5120, 40 heads of 128, FFN 13824; one layer, vocabulary 1000) on the
+    streamed products: [Wq;Wk;Wv] in two token parts per row group (320 workgroups), [Wu;Wg] with four compute waves
+    (216 workgroups), Wo split over K with the residual-norm reduce, and a vocabulary product whose last row block
+    is partial. Every prompt row against the oracle, then 3 decode steps fed the oracle's ids."""
+    from helpers import assert_prefill_ids
+    from test_long_gpu import LOGIT_TOL, _forced_decode, _models
+
+    shape = dict(n_layer=1, dim=5120, n_head=40, ffn=13824, vocab=1000, ctx=128)
+    cfg, ref, model = _models(oracle, vk, ctx, shape, seed=41)
+    try:
+        prompt = oracle.prompt_tokens(42, prompt_len, cfg.vocab)
+        want_ids, want_logits, _ = ref.step(prompt, 0, want_logits=True)
+        ids = model.step(prompt, 0)
+        err = float(np.max(np.abs(model.last_logits(prompt_len).astype(np.float32) -
+                                  want_logits.astype(np.float32))))
+        print(f"[13b streamed] {prompt_len} rows: max|dlogit| {err:.3g}")
+        assert err <= LOGIT_TOL
+        assert_prefill_ids(ids, want_ids, want_logits, f"{prompt_len}-row prompt")
+        worst, ties = _forced_decode(ref, model, want_ids[-1], prompt_len, 3)
+        print(f"[13b streamed] decode max|dlogit| {worst:.3g}, {ties} one-ulp ties")
+        assert ties <= 1
+    finally:
+        ref.close()
+        model.close()
