@@ -94,3 +94,27 @@ def test_prompt_2048_tokens(ctx, vk, oracle, chunks):
     finally:
         ref.close()
         model.close()
+
+
+def test_long_cache_decode_at_7b_widths(ctx, vk, oracle):
+    """The 7B widths (dim 4096, 32 heads of 128, FFN 11008; one layer, vocabulary 1000): a 1030-token prompt (256 x 256
+    tiles with a ragged last row block, the down product split over K), then decode past the 1024-position
+    switch-over on the one-launch long-cache attention (32 heads x 5 chunks, every chunk block resident) with the
+    oracle's ids fed back."""
+    shape = dict(n_layer=1, dim=4096, n_head=32, ffn=11008, vocab=1000, ctx=1100)
+    cfg, ref, model = _models(oracle, vk, ctx, shape, seed=51)
+    try:
+        prompt = oracle.prompt_tokens(52, 1030, cfg.vocab)
+        want_ids, want_logits, _ = ref.step(prompt, 0, want_logits=True)
+        ids = model.step(prompt, 0)
+        err = float(np.max(np.abs(model.last_logits(len(prompt)).astype(np.float32) -
+                                  want_logits.astype(np.float32))))
+        print(f"[7b long] 1030-token prompt: max|dlogit| {err:.3g}", flush=True)
+        assert err <= LOGIT_TOL
+        assert_prefill_ids(ids, want_ids, want_logits, "1030-token prompt")
+        worst, ties = _forced_decode(ref, model, want_ids[-1], len(prompt), 6)
+        print(f"[7b long] decode max|dlogit| {worst:.3g}, {ties} one-ulp ties")
+        assert ties <= 1
+    finally:
+        ref.close()
+        model.close()
