@@ -24,6 +24,9 @@ Printed (one JSON line on stdout):
                launch / its average duration over back-to-back launches across all layers' weights
   cpu_baseline the C oracle (the CPU restatement of the reference's graph, double accumulation) timing greedy
                decode steps of the full-depth model on the host's cores (at most 16 threads)
+  other_configs  (default run only: --config 7b with the workload's own steps and cache, no --no-companions) the
+               7b-long and 13b workloads measured after the headline one in the same process, through the same C
+               loop: their decode tok/s, tok/s near positions 1k/2k/4k, prefill ms, and HBM roofline fractions
 """
 import argparse
 import json
@@ -172,6 +175,89 @@ def cpu_baseline(shape, seconds):
     }
 
 
+def run_workload(ctx, vk, model, shape, prompt_len, steps, warmup, prefill_reps, timing_steps):
+    """Prefill and greedy decode of one workload through the C token loop (vkllm_hip_token_loop, the reference
+    driver's per-token sequence): prompt steps timed one by one, then `steps` decode steps in one timed loop."""
+    prompt = vk.prompt_tokens(PROMPT_SEED, prompt_len, shape["vocab"])
+
+    # prefill: one untimed, then timed repetitions of the same prompt step at offset 0, each through the C token
+    # loop (one step: tensor_new, graph_new, build_graph, init, upload, run, post_run, free)
+    model.loop(prompt, 1)
+    prefill_ns = []
+    for _ in range(prefill_reps):
+        _, sns, _ = model.loop(prompt, 1)
+        prefill_ns.append(int(sns[0]))
+    prefill_s = float(np.median(prefill_ns)) / 1e9
+    log(f"prefill {prompt_len} tokens: {prefill_s * 1e3:.2f} ms (median of {prefill_reps})")
+
+    # decode: prefill + warmup steps untimed, then exactly `steps` single-token steps in one C loop
+    ids, _, _ = model.loop(prompt, 1 + warmup)
+    pos0 = prompt_len + warmup
+    ctx.sync()
+    t0 = time.perf_counter()
+    ids, step_ns, phase_ns = model.loop([int(ids[-1])], steps, offset=pos0)
+    ctx.sync()
+    decode_s = time.perf_counter() - t0
+    pos = pos0 + steps
+    tps = steps / decode_s
+    host = {k: round(float(v) / max(steps - 1, 1) / 1e3, 2)
+            for k, v in zip(("build_us", "init_upload_us", "run_us", "free_us"), phase_ns)}
+    log(f"decode: {steps} steps in {decode_s:.3f} s = {tps:.1f} tok/s; per step {host}")
+    at_positions = {}
+    for target in (1024, 2048, 4096):
+        # the 64 timed steps ending at the target position (or starting there when it is the first one),
+        # from the per-step wall times
+        if steps < 64 or not pos0 <= target <= pos + 1:
+            continue
+        lo = min(max(0, target - pos0 - 64), steps - 64)
+        at_positions[str(target)] = round(64 / (float(np.sum(step_ns[lo:lo + 64])) / 1e9), 1)
+    if at_positions:
+        log(f"decode tok/s near positions: {at_positions}")
+
+    # device time per token: replays of the captured decode graph, back to back, no host work in between
+    # (not available when graph replay is switched off, e.g. VKLLM_GRAPH=0 under a kernel tracer)
+    replay_ns = None
+    if os.environ.get("VKLLM_GRAPH", "1") != "0" and timing_steps > 0:
+        replay_ns = model.time_kernel("decode_step", timing_steps)
+        log(f"decode graph replay: {replay_ns / 1e3:.1f} us per token = {1e9 / replay_ns:.1f} tok/s")
+    return dict(prefill_s=prefill_s, decode_s=decode_s, tps=tps, pos0=pos0, pos=pos, host=host,
+                at_positions=at_positions, replay_ns=replay_ns)
+
+
+def companion(ctx, vk, name, model, prefill_reps, timing_steps):
+    """Another workload measured in the same run, on `model` when given (same shape and cache length), else on a
+    model generated for it: prefill and decode as above, without per-kernel timing or a CPU baseline."""
+    conf = CONFIGS[name]
+    shape = conf["shape"]
+    own = model is None
+    if own:
+        log(f"generating the {name} model on the device")
+        cfg = vk.llama_config(shape["n_layer"], shape["dim"], shape["n_head"], shape["ffn"], shape["vocab"],
+                              conf["ctx"])
+        model = vk.Model(ctx, config=cfg, seed=MODEL_SEED)
+    try:
+        log(f"{name}:")
+        w = run_workload(ctx, vk, model, shape, conf["prompt"], conf["steps"], conf["warmup"], prefill_reps,
+                         timing_steps)
+    finally:
+        if own:
+            model.close()
+    ms = w["decode_s"] / conf["steps"] * 1e3
+    mean_step_bytes = step_bytes(shape, w["pos0"] + conf["steps"] // 2 + 1)
+    return {
+        "workload": conf["name"],
+        "decode_tok_s": round(w["tps"], 2),
+        "steps": conf["steps"],
+        "ms_per_step": round(ms, 4),
+        "decode_positions": [w["pos0"], w["pos"]],
+        "decode_hbm_roofline_frac": round(mean_step_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+        "decode_tok_s_near_position": w["at_positions"] or None,
+        "graph_replay_tok_s_at_last_position": round(1e9 / w["replay_ns"], 1) if w["replay_ns"] else None,
+        "prefill_ms": round(w["prefill_s"] * 1e3, 3),
+        "prefill_tok_s": round(conf["prompt"] / w["prefill_s"], 1),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -182,6 +268,8 @@ def main():
     ap.add_argument("--timing-steps", type=int, default=32, help="graph replays timed for the device-only rate")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline sample length (0: skip)")
     ap.add_argument("--ctx", type=int, default=None, help="KV cache positions (default: the workload's)")
+    ap.add_argument("--no-companions", action="store_true",
+                    help="skip the 7b-long and 13b workloads that the default run also measures")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first run the COPY op on MIB MiB (reference kernel for rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -211,48 +299,9 @@ def main():
     log(f"device {ctx.arch()}; generating the {args.config} model on the device")
     cfg = vk.llama_config(L, shape["dim"], shape["n_head"], shape["ffn"], shape["vocab"], ctx_len)
     model = vk.Model(ctx, config=cfg, seed=MODEL_SEED)
-    prompt = vk.prompt_tokens(PROMPT_SEED, prompt_len, shape["vocab"])
-
-    # prefill: one untimed, then timed repetitions of the same prompt step at offset 0, each through the C token
-    # loop (one step: tensor_new, graph_new, build_graph, init, upload, run, post_run, free)
-    model.loop(prompt, 1)
-    prefill_ns = []
-    for _ in range(args.prefill_reps):
-        _, sns, _ = model.loop(prompt, 1)
-        prefill_ns.append(int(sns[0]))
-    prefill_s = float(np.median(prefill_ns)) / 1e9
-    log(f"prefill {prompt_len} tokens: {prefill_s * 1e3:.2f} ms (median of {args.prefill_reps})")
-
-    # decode: prefill + warmup steps untimed, then exactly `steps` single-token steps in one C loop
-    ids, _, _ = model.loop(prompt, 1 + warmup)
-    pos0 = prompt_len + warmup
-    ctx.sync()
-    t0 = time.perf_counter()
-    ids, step_ns, phase_ns = model.loop([int(ids[-1])], steps, offset=pos0)
-    ctx.sync()
-    decode_s = time.perf_counter() - t0
-    pos = pos0 + steps
-    tps = steps / decode_s
-    host = {k: round(float(v) / max(steps - 1, 1) / 1e3, 2)
-            for k, v in zip(("build_us", "init_upload_us", "run_us", "free_us"), phase_ns)}
-    log(f"decode: {steps} steps in {decode_s:.3f} s = {tps:.1f} tok/s; per step {host}")
-    at_positions = {}
-    for target in (1024, 2048, 4096):
-        # the 64 timed steps ending at the target position (or starting there when it is the first one),
-        # from the per-step wall times
-        if steps < 64 or not pos0 <= target <= pos + 1:
-            continue
-        lo = min(max(0, target - pos0 - 64), steps - 64)
-        at_positions[str(target)] = round(64 / (float(np.sum(step_ns[lo:lo + 64])) / 1e9), 1)
-    if at_positions:
-        log(f"decode tok/s near positions: {at_positions}")
-
-    # device time per token: replays of the captured decode graph, back to back, no host work in between
-    # (not available when graph replay is switched off, e.g. VKLLM_GRAPH=0 under a kernel tracer)
-    replay_ns = None
-    if os.environ.get("VKLLM_GRAPH", "1") != "0" and args.timing_steps > 0:
-        replay_ns = model.time_kernel("decode_step", args.timing_steps)
-        log(f"decode graph replay: {replay_ns / 1e3:.1f} us per token = {1e9 / replay_ns:.1f} tok/s")
+    w = run_workload(ctx, vk, model, shape, prompt_len, steps, warmup, args.prefill_reps, args.timing_steps)
+    prefill_s, decode_s, tps, pos0, pos = w["prefill_s"], w["decode_s"], w["tps"], w["pos0"], w["pos"]
+    host, at_positions, replay_ns = w["host"], w["at_positions"], w["replay_ns"]
 
     # per-kernel durations: back-to-back launches between one hipEvent pair on the library's stream
     nbytes = decode_bytes(shape, pos)
@@ -313,7 +362,22 @@ def main():
                      "algorithmic_bytes": nbytes[dom], "avg_us": round(dom_avg_ns / 1e3, 3)},
         "kernels": kernels,
     }
-    model.close()
+    # the other two workloads, in the default run only: 7b-long on the same model (same shape, 4096-position
+    # cache), then 13b on a model of its own once the 7B one is freed
+    others = None
+    if not args.no_companions and args.config == "7b" and args.steps is None and args.ctx is None:
+        others = {}
+        for name in ("7b-long", "13b"):
+            if name == "13b":
+                model.close()
+                model = None
+            try:
+                others[name] = companion(ctx, vk, name, model, args.prefill_reps, args.timing_steps)
+            except vk.VkllmError as e:
+                others[name] = {"error": str(e)}
+    if model is not None:
+        model.close()
+    result["other_configs"] = others
     ctx.close()
     if args.cpu_seconds > 0:
         log(f"cpu baseline (oracle, full depth, {oracle_threads()} threads)")
