@@ -120,6 +120,10 @@ extern vkllm_err_t vkllm_hip_gemm_noalloc(struct vkllm_context *context, int epi
                                           const uint16_t *B, uint16_t *C, uint32_t M, uint32_t N, uint32_t K,
                                           uint32_t ldc, uint32_t split, uint64_t work_elems);
 
+/* The HIP stream (a hipStream_t) every call on the context enqueues on: the stream a caller captures into a
+ * hipGraph around vkllm_hip_gemm_noalloc, or orders its own work against. */
+extern vkllm_err_t vkllm_hip_context_stream(struct vkllm_context *context, void **stream);
+
 /* Synchronise the context's stream. */
 extern vkllm_err_t vkllm_hip_synchronize(struct vkllm_context *context);
 

@@ -483,6 +483,13 @@ extern "C" vkllm_err_t vkllm_hip_synchronize(struct vkllm_context *ctx)
     return VKLLM_ERR_OK;
 }
 
+extern "C" vkllm_err_t vkllm_hip_context_stream(struct vkllm_context *ctx, void **stream)
+{
+    _CHECK_ARGS(ctx && stream);
+    *stream = (void *)ctx->device->stream;
+    return VKLLM_ERR_OK;
+}
+
 extern "C" const char *vkllm_hip_device_arch(struct vkllm_context *ctx)
 {
     DeviceScope device_scope(ctx);

@@ -772,7 +772,8 @@ static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S
         }
     }
     charge(ctx, fs, NS_LOGITS);
-    if (streamed)
+    // the streamed product stores 4 logits of a row as one 8-byte vector, so its rows of V must stay 8-byte aligned
+    if (streamed && V % 4 == 0)
         KTRY(ctx, KID_F_GEMM, stream_product(st, fs, vk::STREAM_PLAIN, xn, fs->out_t, fs->logits, S, V, D, V));
     else
         KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_PLAIN, fs->xn, mp->out_w, fs->logits, S, V, D, V, 0, cu, fs->gemm_work, kGemmWorkElems));

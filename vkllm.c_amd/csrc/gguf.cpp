@@ -170,6 +170,7 @@ bool File::open(const char *path, std::string *err)
             else
                 for (uint64_t k = 0; k < kv.arr_len && c.ok; ++k)
                     skip(c, kv.arr_type);
+            kv.arr_end = c.p;
         }
         else
         {
@@ -287,9 +288,8 @@ std::vector<std::string> string_array(const KV &kv)
     std::vector<std::string> out;
     if (kv.type != T_ARRAY || kv.arr_type != T_STRING)
         return out;
-    Cursor c{kv.arr_data, kv.arr_data + (size_t)-1 / 2};
-    out.reserve(kv.arr_len);
-    for (uint64_t i = 0; i < kv.arr_len; ++i)
+    Cursor c{kv.arr_data, kv.arr_end};
+    for (uint64_t i = 0; i < kv.arr_len && c.ok; ++i)
         out.push_back(c.str());
     return out;
 }
@@ -297,7 +297,7 @@ std::vector<std::string> string_array(const KV &kv)
 std::vector<float> f32_array(const KV &kv)
 {
     std::vector<float> out;
-    if (kv.type == T_ARRAY && kv.arr_type == T_FLOAT32)
+    if (kv.type == T_ARRAY && kv.arr_type == T_FLOAT32 && (size_t)(kv.arr_end - kv.arr_data) / 4 >= kv.arr_len)
     {
         out.resize(kv.arr_len);
         memcpy(out.data(), kv.arr_data, kv.arr_len * 4);
@@ -308,7 +308,7 @@ std::vector<float> f32_array(const KV &kv)
 std::vector<int32_t> i32_array(const KV &kv)
 {
     std::vector<int32_t> out;
-    if (kv.type == T_ARRAY && kv.arr_type == T_INT32)
+    if (kv.type == T_ARRAY && kv.arr_type == T_INT32 && (size_t)(kv.arr_end - kv.arr_data) / 4 >= kv.arr_len)
     {
         out.resize(kv.arr_len);
         memcpy(out.data(), kv.arr_data, kv.arr_len * 4);

@@ -44,6 +44,7 @@ struct KV
     uint32_t arr_type = 0;
     uint64_t arr_len = 0;
     const uint8_t *arr_data = nullptr; // first element in the mapped file
+    const uint8_t *arr_end = nullptr;  // one past the last element's bytes
 };
 
 struct TensorInfo

@@ -366,6 +366,10 @@ __device__ __forceinline__ void gemv_argmax_finish(const GemvArgs &a, float bv, 
                 v = cv[w];
                 i = ci[w];
             }
+        // Release without a release fence: an agent-scope release compiles to buffer_wbl2 (a write-back of the
+        // whole XCD L2) followed by a vmcnt(0) wait. The write-back is only needed for stores that were not written
+        // through; these two are agent-scope atomic stores (sc1, written through to the level every XCD reads), so
+        // the wait for their completion before the arrival is the whole of what the release has to provide.
         __hip_atomic_store(a.am_val + blockIdx.x, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(a.am_idx + blockIdx.x, i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_s_waitcnt(0);
@@ -374,6 +378,8 @@ __device__ __forceinline__ void gemv_argmax_finish(const GemvArgs &a, float bv, 
     __syncthreads();
     if (!last)
         return;
+    // the last workgroup acquires what every other workgroup published (one cache invalidate, in one workgroup)
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     float v = -INFINITY;
     uint32_t i = 0xFFFFFFFFu;
     for (uint32_t j = tid; j < gridDim.x; j += 256)
@@ -953,9 +959,16 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const uint16_t *logit
     __shared__ uint32_t wi[16];
     const uint32_t t = threadIdx.x;
     const uint16_t *row = logits + (size_t)blockIdx.x * V;
-    // threads without an element hold (-inf, ~0u), which every element precedes
+    // threads without an element hold (-inf, ~0u), which every element precedes. In a row shorter than 32 the
+    // reference's lanes l in [V, 32) enter its reduction with (-FLT_MAX, l) (src/shaders/vkllm_arg_max.comp:55-60),
+    // which wins over a row of -inf: those lanes join here as elements of their own.
     float bv = -INFINITY;
     uint32_t bi = 0xFFFFFFFFu;
+    if (t >= V && t < 32)
+    {
+        bv = -FLT_MAX;
+        bi = t;
+    }
     if ((V & 7u) == 0)
     {
         const u32x4 *rv = (const u32x4 *)row;

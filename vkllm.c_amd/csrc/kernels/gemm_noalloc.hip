@@ -8,13 +8,19 @@
 // current, which looks the array's address up with hipGetSymbolAddress once per device, and the entry point passes
 // that address to the kernels. The split-K partial tiles are written whole before the reduce reads them, so the
 // array needs no clearing between calls; calls that overlap on one GPU (two contexts' streams at once) race on it.
+// Contexts may be created from several threads at once: the per-device address is looked up under a lock and
+// published with release/acquire atomics.
+#include <atomic>
+#include <mutex>
+
 #include "runtime.h"
 
 namespace
 {
 constexpr size_t kNoAllocWorkElems = (size_t)8 << 20;
 __device__ __align__(256) float scratch[kNoAllocWorkElems];
-float *g_scratch[VKLLM_MAX_PHY_DEVS]; // scratch's device address per device, set by noalloc_scratch_init
+std::atomic<float *> g_scratch[VKLLM_MAX_PHY_DEVS]; // scratch's device address per device (noalloc_scratch_init)
+std::mutex g_scratch_lock;
 } // namespace
 
 namespace vk
@@ -23,13 +29,16 @@ hipError_t noalloc_scratch_init(int dev)
 {
     if (dev < 0 || dev >= VKLLM_MAX_PHY_DEVS)
         return hipErrorInvalidDevice;
-    if (g_scratch[dev])
+    if (g_scratch[dev].load(std::memory_order_acquire))
+        return hipSuccess;
+    std::lock_guard<std::mutex> hold(g_scratch_lock);
+    if (g_scratch[dev].load(std::memory_order_relaxed))
         return hipSuccess;
     void *p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess)
         return e;
-    g_scratch[dev] = (float *)p;
+    g_scratch[dev].store((float *)p, std::memory_order_release);
     return hipSuccess;
 }
 } // namespace vk
@@ -52,7 +61,7 @@ extern "C" vkllm_err_t vkllm_hip_gemm_noalloc(struct vkllm_context *ctx, int epi
         return VKLLM_ERR_ARGS;
     }
     const int dev = ctx->device->device_id;
-    float *const work = dev >= 0 && dev < VKLLM_MAX_PHY_DEVS ? g_scratch[dev] : nullptr;
+    float *const work = dev >= 0 && dev < VKLLM_MAX_PHY_DEVS ? g_scratch[dev].load(std::memory_order_acquire) : nullptr;
     if (!work)
     {
         log_error("vkllm_hip_gemm_noalloc: no scratch address for device %d", dev);

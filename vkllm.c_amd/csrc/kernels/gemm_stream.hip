@@ -404,8 +404,8 @@ hipError_t launch_stream_gemm(hipStream_t st, int epi, const uint16_t *X, const 
         if (N % 32 != 0 || ldc < N / 2)
             return hipErrorInvalidValue;
     }
-    else if (epi != STREAM_PLAIN || ldc < N)
-        return hipErrorInvalidValue;
+    else if (epi != STREAM_PLAIN || ldc < N || ldc % 4 != 0 || (uintptr_t)C % 8 != 0)
+        return hipErrorInvalidValue; // the plain store writes 4 outputs of a row as one 8-byte vector
     *splits = n_splits;
     const dim3 grid(groups, n_splits);
     switch (epi)

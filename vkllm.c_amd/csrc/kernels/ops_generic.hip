@@ -407,6 +407,13 @@ __global__ __launch_bounds__(256) void arg_max_kernel(TView in, TView out)
     const uint32_t t = threadIdx.x;
     float bv = -INFINITY;
     uint32_t bi = 0xFFFFFFFFu; // no element: every element comes before it
+    if (t >= W && t < 32)
+    {
+        // the reference's lanes past a row shorter than 32 enter its reduction with (-FLT_MAX, lane)
+        // (src/shaders/vkllm_arg_max.comp:55-60): elements of their own here, ahead of a row of -inf
+        bv = -FLT_MAX;
+        bi = t;
+    }
     for (uint32_t i = t; i < W; i += 256)
     {
         const float v = ldf(in, row + (size_t)i * in.s[3]);

@@ -489,8 +489,11 @@ static bool all_weights_present(const vkllm_models_llama2 *m, const char *file)
     if (!missing && (!m->weights.blocks || m->weights.blocks->used_n != m->meta.block_count))
         missing = "a block";
     if (missing)
+    {
         log_error("gguf %s lacks %s (block %u)", file, missing, layer);
-    return missing == nullptr;
+        return false;
+    }
+    return true;
 }
 
 extern "C" vkllm_err_t vkllm_models_llama2_load(struct vkllm_context *context, struct vkllm_models_llama2 *model,
@@ -1156,15 +1159,23 @@ extern "C" vkllm_err_t vkllm_models_llama2_tokenize(struct vkllm_models_llama2 *
         pieces.erase(pieces.begin() + (long)at + 1);
     }
     _CHECK(vkllm_array_token_id_new(token_ids, pieces.size() + 2));
+    // a failed append frees the partial list and reports the error: no short id list comes back as a success
+    vkllm_err_t err = VKLLM_ERR_OK;
     if (model->meta.add_bos_token)
-        vkllm_array_token_id_append(*token_ids, model->meta.bos_token_id);
-    for (const std::string &p : pieces)
+        err = vkllm_array_token_id_append(*token_ids, model->meta.bos_token_id);
+    for (size_t i = 0; i < pieces.size() && err == VKLLM_ERR_OK; ++i)
     {
-        int id = token_id_of(model, p);
+        int id = token_id_of(model, pieces[i]);
         if (id >= 0)
-            vkllm_array_token_id_append(*token_ids, (uint32_t)id);
+            err = vkllm_array_token_id_append(*token_ids, (uint32_t)id);
     }
-    if (model->meta.add_eos_token)
-        vkllm_array_token_id_append(*token_ids, model->meta.eos_token_id);
-    return VKLLM_ERR_OK;
+    if (err == VKLLM_ERR_OK && model->meta.add_eos_token)
+        err = vkllm_array_token_id_append(*token_ids, model->meta.eos_token_id);
+    if (err != VKLLM_ERR_OK)
+    {
+        log_error("tokenize: appending a token id failed (%s)", vkllm_err_s(err));
+        vkllm_array_token_id_free(*token_ids);
+        *token_ids = nullptr;
+    }
+    return err;
 }

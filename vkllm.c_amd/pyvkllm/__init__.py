@@ -205,6 +205,7 @@ def lib():
             "vkllm_hip_set_graph_replay": (E, [vp, E]),
             "vkllm_hip_set_timing": (E, [vp, E]),
             "vkllm_hip_synchronize": (E, [vp]),
+            "vkllm_hip_context_stream": (E, [vp, ctypes.POINTER(vp)]),
             "vkllm_hip_kernel_stats": (E, [vp, E, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_uint64),
                                            ctypes.POINTER(ctypes.c_uint64)]),
             "vkllm_hip_reset_kernel_stats": (E, [vp]),
