@@ -24,9 +24,14 @@ Printed (one JSON line on stdout):
                launch / its average duration over back-to-back launches across all layers' weights
   cpu_baseline the C oracle (the CPU restatement of the reference's graph, double accumulation) timing greedy
                decode steps of the full-depth model on the host's cores (at most 16 threads)
-  other_configs  (default run only: --config 7b with the workload's own steps and cache, no --no-companions) the
-               7b-long and 13b workloads measured after the headline one in the same process, through the same C
-               loop: their decode tok/s, tok/s near positions 1k/2k/4k, prefill ms, and HBM roofline fractions
+  other_configs  (--config 7b with its own cache length, no --no-companions) the 7b-long and 13b workloads
+               measured after the headline one in the same process, through the same C loop and with their own step
+               counts whatever --steps says: their decode tok/s, tok/s near positions 1k/2k/4k, prefill ms, and HBM
+               roofline fractions
+  isolated_kernels  (--config 7b, no --no-isolated; alone with --isolated-only) the isolated operators through the
+               public VKLLM_OP_* API: GEMV [1x4096].[4096x11008] and [1x4096].[4096x32000], GEMM
+               [512x4096].[4096x4096], RMSNorm [512x4096], RoPE [1,32,512,128]; average launch duration back to back
+               (operands cycled past the 256 MB memory-side cache) and the fraction of the HBM or fp16 MFMA roofline
 """
 import argparse
 import json
@@ -40,6 +45,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(HERE, "vkllm.c_amd"))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+MFMA_FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix cores, TFLOP/s
+CACHE_BYTES = 256 << 20  # MI355X memory-side cache: isolated kernels cycle through more operand bytes than this
 MODEL_SEED, PROMPT_SEED = 0, 1
 ATTN_SMALL_MAX = 1024  # positions up to which the decode attention is the short-cache kernel (VKLLM_ATTN_SMALL_MAX)
 
@@ -175,6 +182,87 @@ def cpu_baseline(shape, seconds):
     }
 
 
+def isolated_kernels(ctx, vk, reps=64):
+    """The isolated-operator workload (fp16 operands, fp32 accumulation, N(0,1) inputs from fixed seeds), each run
+    through the library's public VKLLM_OP_* API (tensor_new + the op) and timed as back-to-back launches between one
+    hipEvent pair (vkllm_hip_time_ops). Every operator cycles through enough copies of its operands that no launch
+    finds them in the GPU's 256 MB memory-side cache. Returns {name: row} with the average launch duration and the
+    fraction of the roofline that bounds it (HBM for the GEMVs, RMSNorm and RoPE; fp16 MFMA for the GEMM)."""
+    rng = np.random.default_rng(20)
+    K = 4096
+    out = {}
+
+    def timed(name, tensors, reps_, work, unit):
+        ns = ctx.time_ops(tensors, reps_) / reps_
+        if unit == "TFLOP/s":
+            achieved, peak = work / ns / 1e3, MFMA_FP16_PEAK_TFLOPS
+            row = {"avg_us": round(ns / 1e3, 3), "flops": work, "achieved": round(achieved, 1), "unit": unit,
+                   "bound": "mfma", "peak": peak}
+        else:
+            achieved, peak = work / ns, HBM_PEAK_GBS
+            row = {"avg_us": round(ns / 1e3, 3), "bytes": work, "achieved": round(achieved, 1), "unit": unit,
+                   "bound": "hbm", "peak": peak}
+        row["frac"] = round(achieved / peak, 4)
+        row["operand_copies"] = len(tensors)
+        out[name] = row
+        log(f"  isolated {name:24s} {ns / 1e3:9.2f} us  {achieved:9.1f} {unit}  {row['frac']:.3f} of peak")
+
+    def normal(shape, dtype=np.float16):
+        return rng.standard_normal(shape, dtype=np.float32).astype(dtype)
+
+    keep = []
+    try:
+        # GEMV [1 x 4096] . [4096 x N] (B stored [N, K], the reference's mat_mul_vec case)
+        x = ctx.tensor_from(normal((1, 1, 1, K)), "x")
+        keep.append(x)
+        for N in (11008, 32000):
+            w = normal((1, 1, N, K))
+            copies = max(1, -(-2 * CACHE_BYTES // w.nbytes))
+            ops = []
+            for c in range(copies):
+                tw = ctx.tensor_from(w, f"w{c}")
+                to = ctx.tensor([1, 1, 1, N], vk.F16, f"y{c}", vk.OP_MATMUL, [x, tw], vk.MatmulParams(1.0, 0))
+                keep += [tw, to]
+                ops.append(to)
+            del w
+            timed(f"gemv_1x{K}x{N}", ops, reps, N * K * 2 + K * 2 + N * 2, "GB/s")
+            for t in keep[1:]:
+                ctx.free(t)
+            keep = keep[:1]
+        # GEMM [512 x 4096] . [4096 x 4096] (B stored [N, K]): matrix-core bound
+        M, N = 512, 4096
+        ta = ctx.tensor_from(normal((1, 1, M, K)), "a")
+        tb = ctx.tensor_from(normal((1, 1, N, K)), "b")
+        tc = ctx.tensor([1, 1, M, N], vk.F16, "c", vk.OP_MATMUL, [ta, tb], vk.MatmulParams(1.0, 0))
+        keep += [ta, tb, tc]
+        timed(f"gemm_{M}x{K}x{N}", [tc], 32, 2 * M * N * K, "TFLOP/s")
+        # RMSNorm over [512 x 4096] (fp16 rows, fp32 weight 1.0) and RoPE over [1, 32, 512, 128] at offset 0
+        xn = normal((1, 1, 512, K))
+        wn = np.ones((1, 1, 1, K), np.float32)
+        xr = normal((1, 32, 512, 128))
+        for name, arr, make, nbytes in (
+                ("rmsnorm_512x4096", xn,
+                 lambda t, w_, c: ctx.tensor([1, 1, 512, K], vk.F16, f"n{c}", vk.OP_RMSNORM, [t, w_],
+                                             vk.RmsnormParams(2.0, 1e-5)), 2 * xn.nbytes + wn.nbytes),
+                ("rope_512x32x128", xr,
+                 lambda t, w_, c: ctx.tensor([1, 32, 512, 128], vk.F16, f"r{c}", vk.OP_ROPE, [t],
+                                             vk.RopeParams(0, 10000.0, False)), 2 * xr.nbytes)):
+            copies = -(-2 * CACHE_BYTES // nbytes)
+            tw = ctx.tensor_from(wn, "norm_w")
+            keep.append(tw)
+            ops = []
+            for c in range(copies):
+                ti = ctx.tensor_from(arr, f"in{c}")
+                to = make(ti, tw, c)
+                keep += [ti, to]
+                ops.append(to)
+            timed(name, ops, 4 * copies, nbytes, "GB/s")
+    finally:
+        for t in keep:
+            ctx.free(t)
+    return out
+
+
 def run_workload(ctx, vk, model, shape, prompt_len, steps, warmup, prefill_reps, timing_steps):
     """Prefill and greedy decode of one workload through the C token loop (vkllm_hip_token_loop, the reference
     driver's per-token sequence): prompt steps timed one by one, then `steps` decode steps in one timed loop."""
@@ -270,6 +358,10 @@ def main():
     ap.add_argument("--ctx", type=int, default=None, help="KV cache positions (default: the workload's)")
     ap.add_argument("--no-companions", action="store_true",
                     help="skip the 7b-long and 13b workloads that the default run also measures")
+    ap.add_argument("--no-isolated", action="store_true",
+                    help="skip the isolated-operator workload that runs with --config 7b")
+    ap.add_argument("--isolated-only", action="store_true",
+                    help="run only the isolated-operator workload (GEMVs, GEMM, RMSNorm, RoPE) and print its line")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first run the COPY op on MIB MiB (reference kernel for rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -294,6 +386,14 @@ def main():
     import pyvkllm as vk
 
     ctx = vk.Ctx(0)
+    if args.isolated_only:
+        log(f"device {ctx.arch()}; isolated operators")
+        iso = isolated_kernels(ctx, vk)
+        ctx.close()
+        print(json.dumps({"metric": "isolated operator kernels, fp16 operands, fp32 accumulation", "n_gpus": 1,
+                          "dtype": "f16 storage, f32 accumulate", "data": "synthetic: N(0,1) operands, fixed seeds",
+                          "isolated_kernels": iso}), flush=True)
+        return
     if args.copy_calibration > 0:
         copy_calibration(ctx, vk, args.copy_calibration)
     log(f"device {ctx.arch()}; generating the {args.config} model on the device")
@@ -365,7 +465,7 @@ def main():
     # the other two workloads, in the default run only: 7b-long on the same model (same shape, 4096-position
     # cache), then 13b on a model of its own once the 7B one is freed
     others = None
-    if not args.no_companions and args.config == "7b" and args.steps is None and args.ctx is None:
+    if not args.no_companions and args.config == "7b" and args.ctx is None:
         others = {}
         for name in ("7b-long", "13b"):
             if name == "13b":
@@ -378,6 +478,10 @@ def main():
     if model is not None:
         model.close()
     result["other_configs"] = others
+    # the isolated operators (GEMVs at the 7B widths, the 512-token GEMM, RMSNorm, RoPE) through the public op API
+    result["isolated_kernels"] = None
+    if not args.no_isolated and args.config == "7b":
+        result["isolated_kernels"] = isolated_kernels(ctx, vk)
     ctx.close()
     if args.cpu_seconds > 0:
         log(f"cpu baseline (oracle, full depth, {oracle_threads()} threads)")

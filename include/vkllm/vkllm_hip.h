@@ -46,6 +46,13 @@ extern vkllm_err_t vkllm_hip_reset_kernel_stats(struct vkllm_context *context);
 extern vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *context, struct vkllm_models_llama2 *model,
                                                const char *family, uint32_t reps, uint64_t *total_ns);
 
+/* Runs the VKLLM_OP_* operator of tensors[r % n] for r < reps back to back between one hipEvent pair on the
+ * context's stream (each tensor is first run once outside the pair) and returns the elapsed nanoseconds: the ops'
+ * kernel time without per-launch synchronisation. Several tensors with their own operands let a caller cycle through
+ * more bytes than the GPU's caches hold. Per-launch timing (vkllm_hip_set_timing) is off inside the pair. */
+extern vkllm_err_t vkllm_hip_time_ops(struct vkllm_context *context, struct vkllm_tensor *const *tensors, uint32_t n,
+                                      uint32_t reps, uint64_t *total_ns);
+
 /* Model configuration for vkllm_models_llama2_init_random. */
 struct vkllm_llama2_config
 {

@@ -122,6 +122,14 @@ int oracle_ffn_up_and_gate(const oracle_tensor *x, const oracle_tensor *wu, cons
  * CPU; 32 in the shader's comments); oracle_set_numerics(0, 0) restores the fp32 mode. Not thread-safe: set it
  * between steps. */
 void oracle_set_numerics(int ref16, uint32_t subgroup);
+/* Summation order of the fp32 mode's model step (projections, RMSNorm sums of squares, attention scores, softmax
+ * sums, P.V). 0 (the default): sums in double, rounded once to fp32, the stand-in for an exact sum that every fp32
+ * order approximates. 1: sums in fp32, one term at a time in index order, the least accurate of the usual orders.
+ * Every rounding to fp16 stays where the reference's graph materialises a tensor; only the sums change. The
+ * reference's own order is its driver's (subgroup trees, tile loops) and nothing pins it, so the distance between
+ * these two orders' outputs is the scale on which a third valid order is judged where one-ulp fp16 differences
+ * accumulate through many layers. Not thread-safe: set it between steps. */
+void oracle_set_accumulation(int fp32_sequential);
 /* fp16 round-to-nearest-even of a double (no double rounding through fp32) */
 uint16_t oracle_f64_to_f16(double v);
 /* src/shaders/vkllm_mat_mul_vec.comp:118-146 f16f16: one output of x[K] . w[K] (K % 4 == 0), times scale, SiLU

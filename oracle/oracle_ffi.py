@@ -90,6 +90,7 @@ def lib():
         L.oracle_token_loop.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32), ctypes.c_uint32,
                                         ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint32), ctypes.c_void_p]
         L.oracle_set_numerics.argtypes = [ctypes.c_int, ctypes.c_uint32]
+        L.oracle_set_accumulation.argtypes = [ctypes.c_int]
         L.oracle_f64_to_f16.restype = ctypes.c_uint16
         L.oracle_f64_to_f16.argtypes = [ctypes.c_double]
         L.oracle_gemv16.restype = ctypes.c_uint16
@@ -113,6 +114,11 @@ def _p16(a):
 def set_numerics(ref16, subgroup=8):
     """REF16 (the reference's fp16-arithmetic shader variants, subgroups of `subgroup` lanes) or the fp32 mode"""
     lib().oracle_set_numerics(1 if ref16 else 0, subgroup if ref16 else 0)
+
+
+def set_accumulation(fp32_sequential):
+    """The fp32 mode's summation order: double sums (False, the default) or sequential fp32 sums (True)"""
+    lib().oracle_set_accumulation(1 if fp32_sequential else 0)
 
 
 def f64_to_f16_bits(x):

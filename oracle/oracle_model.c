@@ -758,6 +758,14 @@ void oracle_set_numerics(int ref16, uint32_t subgroup)
     g_sub = subgroup ? subgroup : 8;
 }
 
+/* the fp32 mode's summation order (oracle.h): 0 double sums, 1 sequential fp32 sums */
+static int g_acc32 = 0;
+
+void oracle_set_accumulation(int fp32_sequential)
+{
+    g_acc32 = fp32_sequential != 0;
+}
+
 uint16_t oracle_f64_to_f16(double d)
 {
     uint64_t x;
@@ -931,10 +939,22 @@ static void linear_row(void *p, size_t n)
     for (uint32_t s = 0; s < j->S; ++s)
     {
         const double *xs = j->xd + (size_t)s * K;
-        double acc = 0.0;
-        for (uint32_t k = 0; k < K; ++k)
-            acc += xs[k] * (double)h2f(w[k]);
-        float v = (float)acc * 1.0f;
+        float v;
+        if (g_acc32)
+        {
+            /* fp16 x fp16 products are exact in fp32; each addition rounds */
+            float acc = 0.f;
+            for (uint32_t k = 0; k < K; ++k)
+                acc += (float)xs[k] * h2f(w[k]);
+            v = acc * 1.0f;
+        }
+        else
+        {
+            double acc = 0.0;
+            for (uint32_t k = 0; k < K; ++k)
+                acc += xs[k] * (double)h2f(w[k]);
+            v = (float)acc * 1.0f;
+        }
         if (j->act)
             v = v / (1.0f + expf(-v));
         j->y[(size_t)s * j->N + n] = oracle_f32_to_f16(v);
@@ -958,12 +978,14 @@ static void rmsnorm_rows(const uint16_t *x, const float *w, uint16_t *y, uint32_
     {
         const uint16_t *xr = x + (size_t)s * D;
         double ss = 0.0;
+        float ss32 = 0.f;
         for (uint32_t i = 0; i < D; ++i)
         {
             double v = h2f(xr[i]);
             ss += v * v;
+            ss32 += (float)v * (float)v;
         }
-        float mean = (float)ss / (float)D;
+        float mean = (g_acc32 ? ss32 : (float)ss) / (float)D;
         float alpha = 1.0f / sqrtf(mean + eps);
         for (uint32_t i = 0; i < D; ++i)
             y[(size_t)s * D + i] = oracle_f32_to_f16((h2f(xr[i]) * w[i]) * alpha);
@@ -1032,18 +1054,26 @@ static void attn_row(void *p, size_t i)
     {
         const uint16_t *kr = kc + ((size_t)hh * ctx + j) * hd;
         double acc = 0.0;
+        float acc32 = 0.f;
         for (uint32_t d = 0; d < hd; ++d)
+        {
             acc += (double)h2f(qr[d]) * (double)h2f(kr[d]);
-        sc[j] = oracle_f32_to_f16((float)acc * scale);
+            acc32 += h2f(qr[d]) * h2f(kr[d]);
+        }
+        sc[j] = oracle_f32_to_f16((g_acc32 ? acc32 : (float)acc) * scale);
     }
     /* SOFTMAX seq_mask=1, offsets=offset (layers.c:237-245, softmax.comp:53-95) */
     float mx = h2f(sc[0]);
     for (uint32_t j = 0; j < kv; ++j)
         mx = h2f(sc[j]) > mx ? h2f(sc[j]) : mx;
     double sum = 0.0;
+    float sum32 = 0.f;
     for (uint32_t j = 0; j <= s + offset && j < kv; ++j)
+    {
         sum += expf(h2f(sc[j]) - mx);
-    float sf = (float)sum;
+        sum32 += expf(h2f(sc[j]) - mx);
+    }
+    float sf = g_acc32 ? sum32 : (float)sum;
     for (uint32_t j = 0; j < kv; ++j)
         pr[j] = j > s + offset ? 0 : oracle_f32_to_f16(expf(h2f(sc[j]) - mx) / sf);
     /* attn . V (layers.c:247-257). When kv == hd, is_transposed_b (src/core/vkllm_op_matmul.c:14-24)
@@ -1052,13 +1082,15 @@ static void attn_row(void *p, size_t i)
     for (uint32_t n = 0; n < hd; ++n)
     {
         double acc = 0.0;
+        float acc32 = 0.f;
         for (uint32_t j = 0; j < kv; ++j)
         {
             uint16_t vv = transposed ? vc[((size_t)hh * ctx + n) * hd + j] : vc[((size_t)hh * ctx + j) * hd + n];
             acc += (double)h2f(pr[j]) * (double)h2f(vv);
+            acc32 += h2f(pr[j]) * h2f(vv);
         }
         /* permute + COPY into [S, H*hd] (layers.c:259-281) */
-        att[(size_t)s * D + (size_t)hh * hd + n] = oracle_f32_to_f16((float)acc * 1.0f);
+        att[(size_t)s * D + (size_t)hh * hd + n] = oracle_f32_to_f16((g_acc32 ? acc32 : (float)acc) * 1.0f);
     }
 
     free(sc);

@@ -505,3 +505,74 @@ def test_oracle_token_loop_planted_offset_error_is_caught(oracle):
         seq.append(int(out[-1]))
         toks = np.array([seq[-1]], np.uint32)
     assert worst > 2e-2  # the recompute check's tolerance
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# the fp32 mode's two summation orders (oracle_set_accumulation): double sums, or sequential fp32 sums
+def _zero_layer_model(path, out_rows, dim=64, n_head=2, ffn=64):
+    """A one-layer GGUF whose projection weights are all zero, so the residual stream stays the embedding row; the
+    embedding rows are all 1.0 (RMSNorm of such a row is exactly 1.0 in fp16), so logit n is the plain sum of output
+    row n, added in index order by the sequential mode."""
+    import gguf_util as G
+
+    V = len(out_rows)
+    z = lambda r, c: np.zeros((r, c), np.float16)
+    ones32 = np.ones(dim, np.float32)
+    kvs = [("general.architecture", G.STRING, "llama"), ("llama.block_count", G.U32, 1),
+           ("llama.context_length", G.U32, 8), ("llama.embedding_length", G.U32, dim),
+           ("llama.feed_forward_length", G.U32, ffn), ("llama.attention.head_count", G.U32, n_head),
+           ("llama.attention.head_count_kv", G.U32, n_head), ("llama.attention.layer_norm_rms_epsilon", G.F32, 1e-5),
+           ("llama.rope.freq_base", G.F32, 10000.0), ("llama.vocab_size", G.U32, V)]
+    out = np.zeros((V, dim), np.float16)
+    for n, row in enumerate(out_rows):
+        out[n, :len(row)] = row
+    tensors = [("token_embd.weight", [dim, V], G.GGML_F16, np.ones((V, dim), np.float16)),
+               ("blk.0.attn_norm.weight", [dim], G.GGML_F32, ones32)]
+    tensors += [(f"blk.0.{n}.weight", [dim, dim], G.GGML_F16, z(dim, dim)) for n in ("attn_q", "attn_k", "attn_v",
+                                                                                        "attn_output")]
+    tensors += [("blk.0.ffn_norm.weight", [dim], G.GGML_F32, ones32),
+                ("blk.0.ffn_gate.weight", [dim, ffn], G.GGML_F16, z(ffn, dim)),
+                ("blk.0.ffn_up.weight", [dim, ffn], G.GGML_F16, z(ffn, dim)),
+                ("blk.0.ffn_down.weight", [ffn, dim], G.GGML_F16, z(dim, ffn)),
+                ("output_norm.weight", [dim], G.GGML_F32, ones32), ("output.weight", [dim, V], G.GGML_F16, out)]
+    G.write(str(path), kvs, tensors)
+
+
+def test_sequential_fp32_accumulation_known_answers(oracle, tmp_path):
+    """32768 + 2^-10 rounds back to 32768 in fp32 (2^-10 is under half of 32768's fp32 spacing 2^-8), so a
+    sequential fp32 sum of [32768, 2^-10, -32768] is 0 while the double sum is 2^-10; in the order
+    [32768, -32768, 2^-10] both give 2^-10; a sum that never leaves fp32's exact range agrees in both."""
+    t = 2.0 ** -10
+    rows = [[32768, t, -32768], [32768, -32768, t], [1.0] * 64, [0.5, 0.25, 0.125]]
+    path = tmp_path / "zero_layer.gguf"
+    _zero_layer_model(path, rows)
+    got = {}
+    for mode in (False, True):
+        oracle.set_accumulation(mode)
+        try:
+            m = oracle.Model(str(path))
+            _, logits, _ = m.step(np.array([0], np.uint32), 0, want_logits=True)
+            m.close()
+        finally:
+            oracle.set_accumulation(False)
+        got[mode] = logits[0].astype(np.float64)
+    assert got[False].tolist() == [t, t, 64.0, 0.875]
+    assert got[True].tolist() == [0.0, t, 64.0, 0.875]
+
+
+def test_sequential_fp32_order_is_the_same_graph(oracle):
+    """The two orders differ only by fp32 rounding: over two layers at a small width their logits agree within the
+    2e-2 bar but not bit for bit (the switch reaches the model step)."""
+    cfg = oracle.make_cfg(n_layer=2, dim=256, n_head=4, ffn=512, vocab=500, ctx=64)
+    toks = oracle.prompt_tokens(3, 24, cfg.vocab)
+    out = {}
+    for mode in (False, True):
+        oracle.set_accumulation(mode)
+        try:
+            m = oracle.Model(cfg=cfg, seed=11)
+            _, out[mode], _ = m.step(toks, 0, want_logits=True)
+            m.close()
+        finally:
+            oracle.set_accumulation(False)
+    d = np.abs(out[True].astype(np.float64) - out[False].astype(np.float64))
+    assert 0 < d.max() < 2e-2

@@ -431,6 +431,8 @@ extern "C" void vkllm_context_free(struct vkllm_context *ctx)
             (void)timing_flush(ctx);
         for (hipEvent_t e : ctx->device->event_pool)
             (void)hipEventDestroy(e);
+        if (ctx->device->op_work)
+            (void)hipFree(ctx->device->op_work);
         pool_release_all(ctx->device);
         node_pool_release(ctx->device);
         if (ctx->device->stream)

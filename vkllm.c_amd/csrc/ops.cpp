@@ -233,7 +233,19 @@ extern "C" vkllm_err_t vkllm_op_rmsnorm_run(struct vkllm_context *context, struc
     NEED_DEV(x);
     NEED_DEV(w);
     NEED_DEV(out);
-    LAUNCH(context, KID_RMSNORM, vk::launch_rmsnorm(context->device->stream, x, w, out, p.eps));
+    // contiguous rows of a multiple of 8 take the fused step's row kernel (512 threads, 16-byte vectors)
+    const uint32_t D = x.n[3];
+    const uint64_t rows = (uint64_t)x.n[0] * x.n[1] * x.n[2];
+    auto packed = [D](const vk::TView &v) {
+        return v.s[3] == 1 && v.s[2] == D && v.s[1] == v.n[2] * D && v.s[0] == v.n[1] * v.s[1] &&
+               (uintptr_t)v.p % 16 == 0;
+    };
+    if (D % 8 == 0 && rows <= 0x7fffffffu && packed(x) && packed(out) && w.s[3] == 1 && (uintptr_t)w.p % 16 == 0)
+        LAUNCH(context, KID_RMSNORM,
+               vk::launch_rmsnorm_rows(context->device->stream, (const uint16_t *)x.p, (const float *)w.p,
+                                       (uint16_t *)out.p, (uint32_t)rows, D, p.eps, false));
+    else
+        LAUNCH(context, KID_RMSNORM, vk::launch_rmsnorm(context->device->stream, x, w, out, p.eps));
     commands_note_write(commands, tensor);
     return VKLLM_ERR_OK;
 }
@@ -259,6 +271,71 @@ static bool is_transposed_b(const vkllm_tensor *t)
 static bool is_mat_mul_vec(const vkllm_tensor *t)
 {
     return t->srcs[0]->shapes[2] == 1 && is_transposed_b(t);
+}
+
+// The matrix-core and streaming kernels of the fused token step serve the op when its operands have their layout:
+// fp16 A [1,1,M,K], B [1,1,N,K] (is_transposed_b) and out [1,1,M,N], rows contiguous, K a multiple of 8, 16-byte
+// aligned rows, scale 1. M == 1 (the reference's mat_mul_vec case) takes the streaming GEMV (16-byte weight loads,
+// fp32 accumulation, DPP wave sums) when act is 0; M > 1 takes the MFMA tile GEMM, act 1 as its SiLU epilogue.
+// Anything else (fp32, broadcast batches, B as [K, N], a scale, strided views) runs the generic kernels. Both keep
+// the reference's rounding points (fp32 sums, then fp16(act(scale * acc))), so only the fp32 summation order differs.
+enum MatmulPath
+{
+    GENERIC,
+    FAST_GEMV,
+    FAST_GEMM
+};
+
+static bool rows_fp16(const vk::TView &v, uint32_t rows, uint32_t cols)
+{
+    return v.dt == vkllm_dtype_float16 && v.n[0] == 1 && v.n[1] == 1 && v.n[2] == rows && v.n[3] == cols &&
+           v.s[3] == 1 && (rows == 1 || v.s[2] % 8 == 0) && (uintptr_t)v.p % 16 == 0;
+}
+
+static MatmulPath matmul_fast_path(const vk::TView &a, const vk::TView &b, const vk::TView &out,
+                                   const vkllm_op_matmul_params &p, bool transposed_b)
+{
+    const uint32_t M = out.n[2], N = out.n[3], K = a.n[3];
+    if (!transposed_b || p.scale != 1.0f || K % 8 != 0 || !rows_fp16(a, M, K) || !rows_fp16(b, N, K) ||
+        !rows_fp16(out, M, N) || (M > 1 && a.s[2] != K) || b.s[2] != K)
+        return GENERIC;
+    if (M == 1)
+        return p.act == 0 ? FAST_GEMV : GENERIC;
+    return p.act == 0 || p.act == 1 ? FAST_GEMM : GENERIC;
+}
+
+static hipError_t launch_op_gemv(vkllm_context *ctx, const vk::TView &a, const vk::TView &b, const vk::TView &out)
+{
+    vk::GemvArgs g{};
+    g.x = (const uint16_t *)a.p;
+    g.w = (const uint16_t *)b.p;
+    g.K = a.n[3];
+    g.rows = out.n[3];
+    g.units = (g.rows + 1) / 2;
+    g.out = (uint16_t *)out.p;
+    return vk::launch_gemv(ctx->device->stream, vk::EPI_PLAIN, g, ctx->device->cu_count);
+}
+
+// 64 MB of split-K partials for the op's tile GEMM, made once per context (the kernels then split K only as far as
+// it fits); an allocation failure leaves K unsplit
+static vkllm_err_t op_gemm_workspace(vkllm_context *ctx, float **work, size_t *elems)
+{
+    vkllm_gpu_device *dev = ctx->device;
+    if (!dev->op_work)
+    {
+        const size_t want = (size_t)16 << 20;
+        if (hipMalloc(&dev->op_work, want * sizeof(float)) == hipSuccess)
+            dev->op_work_elems = want;
+        else
+        {
+            (void)hipGetLastError();
+            dev->op_work = nullptr;
+            dev->op_work_elems = 0;
+        }
+    }
+    *work = dev->op_work;
+    *elems = dev->op_work_elems;
+    return VKLLM_ERR_OK;
 }
 
 extern "C" vkllm_err_t vkllm_op_matmul_init(struct vkllm_context *context, struct vkllm_commands *commands,
@@ -309,8 +386,26 @@ extern "C" vkllm_err_t vkllm_op_matmul_run(struct vkllm_context *context, struct
     NEED_DEV(av);
     NEED_DEV(bv);
     NEED_DEV(out);
-    LAUNCH(context, is_mat_mul_vec(tensor) ? KID_GEMV : KID_GEMM,
-           vk::launch_matmul(context->device->stream, av, bv, out, p.scale, p.act, tb));
+    const KernelId kid = is_mat_mul_vec(tensor) ? KID_GEMV : KID_GEMM;
+    switch (matmul_fast_path(av, bv, out, p, tb))
+    {
+    case FAST_GEMV:
+        LAUNCH(context, kid, launch_op_gemv(context, av, bv, out));
+        break;
+    case FAST_GEMM:
+    {
+        float *work = nullptr;
+        size_t work_elems = 0;
+        _CHECK(op_gemm_workspace(context, &work, &work_elems));
+        LAUNCH(context, kid,
+               vk::launch_gemm(context->device->stream, p.act ? vk::GEMM_SILU_HI : vk::GEMM_PLAIN,
+                               (const uint16_t *)av.p, (const uint16_t *)bv.p, (uint16_t *)out.p, M, N, K, out.s[2], 0,
+                               context->device->cu_count, work, work_elems));
+        break;
+    }
+    default:
+        LAUNCH(context, kid, vk::launch_matmul(context->device->stream, av, bv, out, p.scale, p.act, tb));
+    }
     commands_note_write(commands, tensor);
     return VKLLM_ERR_OK;
 }
@@ -642,4 +737,42 @@ vkllm_err_t op_post_run(vkllm_context *ctx, vkllm_commands *cmds, vkllm_tensor *
         return VKLLM_ERR_ARGS;
     }
     return VKLLM_ERR_OK;
+}
+
+// =============================================================================================================
+// vkllm_hip_time_ops (vkllm_hip.h): back-to-back op launches between one hipEvent pair on the context's stream
+extern "C" vkllm_err_t vkllm_hip_time_ops(struct vkllm_context *context, struct vkllm_tensor *const *tensors,
+                                          uint32_t n, uint32_t reps, uint64_t *total_ns)
+{
+    DeviceScope device_scope(context);
+    _CHECK_ARGS(context && tensors && n > 0 && reps > 0 && total_ns);
+    vkllm_commands *cmds = nullptr;
+    _CHECK(vkllm_commands_new(context, &cmds));
+    vkllm_gpu_device *dev = context->device;
+    const int timing = dev->timing;
+    dev->timing = 0; // no per-launch events inside the timed region
+    hipEvent_t b = nullptr, e = nullptr;
+    vkllm_err_t rc = VKLLM_ERR_OK;
+    // every op once first: argument checks, and first-use allocations stay outside the region
+    for (uint32_t i = 0; i < n && rc == VKLLM_ERR_OK; ++i)
+        rc = tensors[i] ? op_run(context, cmds, tensors[i]) : VKLLM_ERR_ARGS;
+    if (rc == VKLLM_ERR_OK && (hipEventCreate(&b) != hipSuccess || hipEventCreate(&e) != hipSuccess ||
+                               hipEventRecord(b, dev->stream) != hipSuccess))
+        rc = VKLLM_ERR_VULKAN;
+    for (uint32_t r = 0; r < reps && rc == VKLLM_ERR_OK; ++r)
+        rc = op_run(context, cmds, tensors[r % n]);
+    float ms = 0.f;
+    if (rc == VKLLM_ERR_OK && (hipEventRecord(e, dev->stream) != hipSuccess || hipEventSynchronize(e) != hipSuccess ||
+                               hipEventElapsedTime(&ms, b, e) != hipSuccess))
+        rc = VKLLM_ERR_VULKAN;
+    if (rc == VKLLM_ERR_OK)
+        *total_ns = (uint64_t)((double)ms * 1e6);
+    (void)hipStreamSynchronize(dev->stream);
+    if (b)
+        (void)hipEventDestroy(b);
+    if (e)
+        (void)hipEventDestroy(e);
+    dev->timing = timing;
+    vkllm_commands_free(context, cmds);
+    return rc;
 }

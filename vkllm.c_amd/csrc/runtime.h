@@ -93,6 +93,9 @@ struct vkllm_gpu_device
     vkllm_pipeline *timing_node = nullptr;
     std::vector<TimingRec> timing_pending;
     std::vector<hipEvent_t> event_pool;
+    // split-K partial tiles of the MATMUL op's matrix-core path, allocated at its first use (op_gemm_workspace)
+    float *op_work = nullptr;
+    size_t op_work_elems = 0;
 };
 
 // ---- errors ----

@@ -206,6 +206,7 @@ def lib():
             "vkllm_hip_set_timing": (E, [vp, E]),
             "vkllm_hip_synchronize": (E, [vp]),
             "vkllm_hip_context_stream": (E, [vp, ctypes.POINTER(vp)]),
+            "vkllm_hip_time_ops": (E, [vp, ctypes.POINTER(TensorP), u32, u32, ctypes.POINTER(ctypes.c_uint64)]),
             "vkllm_hip_kernel_stats": (E, [vp, E, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_uint64),
                                            ctypes.POINTER(ctypes.c_uint64)]),
             "vkllm_hip_reset_kernel_stats": (E, [vp]),
@@ -345,6 +346,13 @@ class Ctx:
             if n.value:
                 out[name.value.decode()] = (n.value, ns.value)
         return out
+
+    def time_ops(self, tensors, reps):
+        """Nanoseconds of `reps` back-to-back runs of the ops of `tensors` (cycled) between one event pair."""
+        arr = (TensorP * len(tensors))(*tensors)
+        ns = ctypes.c_uint64()
+        check("vkllm_hip_time_ops", lib().vkllm_hip_time_ops(self.vp, arr, len(tensors), reps, ctypes.byref(ns)))
+        return ns.value
 
     def reset_kernel_stats(self):
         check("vkllm_hip_reset_kernel_stats", lib().vkllm_hip_reset_kernel_stats(self.vp))
