@@ -936,28 +936,76 @@ static void linear_row(void *p, size_t n)
         }
         return;
     }
-    for (uint32_t s = 0; s < j->S; ++s)
+    /* The weight row is converted once, then TB tokens at a time: every output keeps its own sum, added in k order
+     * exactly as for one token alone (the tokens' independent chains only overlap in time). */
+    enum
     {
-        const double *xs = j->xd + (size_t)s * K;
-        float v;
-        if (g_acc32)
+        TB = 8
+    };
+    double wd[K];
+    float wf[K];
+    if (j->S >= TB) /* a single token reads the row directly (one pass over the weights) */
+        for (uint32_t k = 0; k < K; ++k)
         {
-            /* fp16 x fp16 products are exact in fp32; each addition rounds */
-            float acc = 0.f;
-            for (uint32_t k = 0; k < K; ++k)
-                acc += (float)xs[k] * h2f(w[k]);
-            v = acc * 1.0f;
+            wf[k] = h2f(w[k]);
+            wd[k] = wf[k];
+        }
+    for (uint32_t s0 = 0; s0 < j->S;)
+    {
+        /* TB tokens at once while that many remain, then one at a time */
+        const uint32_t nb = j->S - s0 >= TB ? TB : 1;
+        float v[TB];
+        if (nb == TB)
+        {
+            const double *xs[TB];
+            for (uint32_t t = 0; t < TB; ++t)
+                xs[t] = j->xd + (size_t)(s0 + t) * K;
+            if (g_acc32)
+            {
+                /* fp16 x fp16 products are exact in fp32; each addition rounds */
+                float acc[TB] = {0};
+                for (uint32_t k = 0; k < K; ++k)
+                    for (uint32_t t = 0; t < TB; ++t)
+                        acc[t] += (float)xs[t][k] * wf[k];
+                for (uint32_t t = 0; t < TB; ++t)
+                    v[t] = acc[t] * 1.0f;
+            }
+            else
+            {
+                double acc[TB] = {0};
+                for (uint32_t k = 0; k < K; ++k)
+                    for (uint32_t t = 0; t < TB; ++t)
+                        acc[t] += xs[t][k] * wd[k];
+                for (uint32_t t = 0; t < TB; ++t)
+                    v[t] = (float)acc[t] * 1.0f;
+            }
         }
         else
         {
-            double acc = 0.0;
-            for (uint32_t k = 0; k < K; ++k)
-                acc += xs[k] * (double)h2f(w[k]);
-            v = (float)acc * 1.0f;
+            const double *xs = j->xd + (size_t)s0 * K;
+            if (g_acc32)
+            {
+                float acc = 0.f;
+                for (uint32_t k = 0; k < K; ++k)
+                    acc += (float)xs[k] * h2f(w[k]);
+                v[0] = acc * 1.0f;
+            }
+            else
+            {
+                double acc = 0.0;
+                for (uint32_t k = 0; k < K; ++k)
+                    acc += xs[k] * (double)h2f(w[k]);
+                v[0] = (float)acc * 1.0f;
+            }
         }
-        if (j->act)
-            v = v / (1.0f + expf(-v));
-        j->y[(size_t)s * j->N + n] = oracle_f32_to_f16(v);
+        for (uint32_t t = 0; t < nb; ++t)
+        {
+            float y = v[t];
+            if (j->act)
+                y = y / (1.0f + expf(-y));
+            j->y[(size_t)(s0 + t) * j->N + n] = oracle_f32_to_f16(y);
+        }
+        s0 += nb;
     }
 }
 
@@ -1049,16 +1097,45 @@ static void attn_row(void *p, size_t i)
         return;
     }
 
-    /* scores = fp16(scale * q.k) (src/models/vkllm_llama2_layers.c:223-233) */
-    for (uint32_t j = 0; j < kv; ++j)
+    /* scores = fp16(scale * q.k) (src/models/vkllm_llama2_layers.c:223-233). Four keys at a time: each score keeps
+     * its own sum over d in order (the keys' independent chains only overlap in time). */
+    float qf[hd];
+    for (uint32_t d = 0; d < hd; ++d)
+        qf[d] = h2f(qr[d]);
+    uint32_t j0 = 0;
+    for (; j0 + 4 <= kv; j0 += 4)
+    {
+        const uint16_t *kr[4];
+        for (int t = 0; t < 4; ++t)
+            kr[t] = kc + ((size_t)hh * ctx + j0 + t) * hd;
+        if (g_acc32)
+        {
+            float acc[4] = {0};
+            for (uint32_t d = 0; d < hd; ++d)
+                for (int t = 0; t < 4; ++t)
+                    acc[t] += qf[d] * h2f(kr[t][d]);
+            for (int t = 0; t < 4; ++t)
+                sc[j0 + t] = oracle_f32_to_f16(acc[t] * scale);
+        }
+        else
+        {
+            double acc[4] = {0};
+            for (uint32_t d = 0; d < hd; ++d)
+                for (int t = 0; t < 4; ++t)
+                    acc[t] += (double)qf[d] * (double)h2f(kr[t][d]);
+            for (int t = 0; t < 4; ++t)
+                sc[j0 + t] = oracle_f32_to_f16((float)acc[t] * scale);
+        }
+    }
+    for (uint32_t j = j0; j < kv; ++j)
     {
         const uint16_t *kr = kc + ((size_t)hh * ctx + j) * hd;
         double acc = 0.0;
         float acc32 = 0.f;
         for (uint32_t d = 0; d < hd; ++d)
         {
-            acc += (double)h2f(qr[d]) * (double)h2f(kr[d]);
-            acc32 += h2f(qr[d]) * h2f(kr[d]);
+            acc += (double)qf[d] * (double)h2f(kr[d]);
+            acc32 += qf[d] * h2f(kr[d]);
         }
         sc[j] = oracle_f32_to_f16((g_acc32 ? acc32 : (float)acc) * scale);
     }
@@ -1077,20 +1154,31 @@ static void attn_row(void *p, size_t i)
     for (uint32_t j = 0; j < kv; ++j)
         pr[j] = j > s + offset ? 0 : oracle_f32_to_f16(expf(h2f(sc[j]) - mx) / sf);
     /* attn . V (layers.c:247-257). When kv == hd, is_transposed_b (src/core/vkllm_op_matmul.c:14-24)
-     * reads the [kv, hd] V slice as [N, K] and the product becomes attn . V^T. */
+     * reads the [kv, hd] V slice as [N, K] and the product becomes attn . V^T. Eight outputs at a time, each summed
+     * over j in order. */
     int transposed = (kv == hd);
-    for (uint32_t n = 0; n < hd; ++n)
+    const uint16_t *vh = vc + (size_t)hh * ctx * hd;
+    for (uint32_t n0 = 0; n0 < hd; n0 += 8)
     {
-        double acc = 0.0;
-        float acc32 = 0.f;
+        const uint32_t nb = hd - n0 < 8 ? hd - n0 : 8;
+        double acc[8] = {0};
+        float acc32[8] = {0};
         for (uint32_t j = 0; j < kv; ++j)
         {
-            uint16_t vv = transposed ? vc[((size_t)hh * ctx + n) * hd + j] : vc[((size_t)hh * ctx + j) * hd + n];
-            acc += (double)h2f(pr[j]) * (double)h2f(vv);
-            acc32 += h2f(pr[j]) * h2f(vv);
+            const float p = h2f(pr[j]);
+            for (uint32_t t = 0; t < nb; ++t)
+            {
+                const uint16_t vv = transposed ? vh[(size_t)(n0 + t) * hd + j] : vh[(size_t)j * hd + n0 + t];
+                if (g_acc32)
+                    acc32[t] += p * h2f(vv);
+                else
+                    acc[t] += (double)p * (double)h2f(vv);
+            }
         }
         /* permute + COPY into [S, H*hd] (layers.c:259-281) */
-        att[(size_t)s * D + (size_t)hh * hd + n] = oracle_f32_to_f16((g_acc32 ? acc32 : (float)acc) * 1.0f);
+        for (uint32_t t = 0; t < nb; ++t)
+            att[(size_t)s * D + (size_t)hh * hd + n0 + t] =
+                oracle_f32_to_f16((g_acc32 ? acc32[t] : (float)acc[t]) * 1.0f);
     }
 
     free(sc);

@@ -66,6 +66,7 @@ def _forced_decode(ref, model, first_tok, offset, n, what):
     return worst, ties, tok
 
 
+@pytest.mark.timeout(600)  # the oracle's 2048-token step at the 13B widths runs on the host's cores
 def test_13b_widths_2048_token_prompt(ctx, vk, oracle):
     shape = dict(n_layer=1, dim=5120, n_head=40, ffn=13824, vocab=1000, ctx=2176)
     cfg, ref, model = _models(oracle, vk, ctx, shape, seed=61)
@@ -80,6 +81,7 @@ def test_13b_widths_2048_token_prompt(ctx, vk, oracle):
         model.close()
 
 
+@pytest.mark.timeout(600)  # the oracle's 4000-token prompt at the 7B widths runs on the host's cores
 def test_7b_widths_decode_to_4096_positions(ctx, vk, oracle):
     shape = dict(n_layer=1, dim=4096, n_head=32, ffn=11008, vocab=1000, ctx=4096)
     cfg, ref, model = _models(oracle, vk, ctx, shape, seed=71)

@@ -68,6 +68,7 @@ def _gpu_forced(ctx, vk, shape, prompt, forced):
     return np.concatenate(rows).astype(np.float32), c_ids
 
 
+@pytest.mark.timeout(900)  # the oracle runs the full depth twice on the host's cores
 @pytest.mark.parametrize("name", sorted(CASES))
 def test_full_depth(ctx, vk, oracle, monkeypatch, name):
     shape, prompt_len, n_steps = CASES[name]

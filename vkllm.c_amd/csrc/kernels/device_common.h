@@ -237,6 +237,44 @@ __device__ __forceinline__ void rmsnorm_row_to(const uint16_t *x, const float *w
 {
     const uint32_t nv = D / 8;
     const u32x4 *xv = (const u32x4 *)x;
+    const float4 *wv = (const float4 *)w;
+    if (nv <= blockDim.x)
+    {
+        // one vector per thread: the row and its weights are read once, before the reduction, and kept in
+        // registers (the same sums in the same order as the loop below)
+        const uint32_t i = threadIdx.x;
+        u32x4 v = (u32x4){0, 0, 0, 0};
+        float4 w0 = {0.f, 0.f, 0.f, 0.f}, w1 = w0;
+        if (i < nv)
+        {
+            v = xv[i];
+            w0 = wv[2 * i];
+            w1 = wv[2 * i + 1];
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+        {
+            float a = half_lo(v[k]), b = half_hi(v[k]);
+            ss += a * a;
+            ss += b * b;
+        }
+        ss = block_sum(ss, red);
+        const float alpha = 1.0f / sqrtf(ss / (float)D + eps);
+        if (i < nv)
+        {
+            const float ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+            u32x4 o;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+            {
+                float a = half_lo(v[k]), b = half_hi(v[k]);
+                o[k] = pack2(f2h((a * ws[2 * k]) * alpha), f2h((b * ws[2 * k + 1]) * alpha));
+            }
+            dst[xt_row < 0 ? i : xt_vec((uint32_t)xt_row, i)] = o;
+        }
+        return;
+    }
     float ss = 0.f;
     for (uint32_t i = threadIdx.x; i < nv; i += blockDim.x)
     {
@@ -251,7 +289,6 @@ __device__ __forceinline__ void rmsnorm_row_to(const uint16_t *x, const float *w
     }
     ss = block_sum(ss, red);
     const float alpha = 1.0f / sqrtf(ss / (float)D + eps);
-    const float4 *wv = (const float4 *)w;
     for (uint32_t i = threadIdx.x; i < nv; i += blockDim.x)
     {
         u32x4 v = xv[i];

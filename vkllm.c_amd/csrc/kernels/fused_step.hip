@@ -233,6 +233,7 @@ hipError_t launch_gemv_loop(hipStream_t st, int epi, const GemvArgs &a, int cu_c
     switch (epi)
     {
     case EPI_PLAIN:
+    case EPI_RAW: // the plain kernel normalises only when norm_w is given
         gemv_kernel<EPI_PLAIN><<<blocks, 256, lds, st>>>(a);
         break;
     case EPI_RESID:
@@ -275,7 +276,7 @@ template <int EPI, int R> __device__ __forceinline__ void gemv_epilogue(const Ge
                                                                         const uint32_t *rows, const float *acc,
                                                                         const float *fq, const float *rs)
 {
-    if (EPI == EPI_PLAIN || EPI == EPI_ARGMAX)
+    if (EPI == EPI_PLAIN || EPI == EPI_ARGMAX || EPI == EPI_RAW)
     {
 #pragma unroll
         for (int k = 0; k < R; ++k)
@@ -337,7 +338,7 @@ template <int EPI, int R> __device__ __forceinline__ void gemv_epilogue(const Ge
 // the epilogues whose input is the RMSNorm of the residual stream (all but the residual products)
 constexpr bool gemv_normalises(int epi)
 {
-    return epi != EPI_RESID;
+    return epi != EPI_RESID && epi != EPI_RAW;
 }
 
 // EPI_ARGMAX after the workgroup's last unit: (bv, bi) is lane 0's best of its wave's rows. The workgroup's best goes
@@ -712,6 +713,8 @@ hipError_t launch_gemv(hipStream_t st, int epi, const GemvArgs &a, int cu_count)
         {
         case EPI_PLAIN:
             return launch_epi<EPI_PLAIN>(st, a, cu_count, R, NV);
+        case EPI_RAW:
+            return launch_epi<EPI_RAW>(st, a, cu_count, R, NV);
         case EPI_RESID:
             return launch_epi<EPI_RESID>(st, a, cu_count, R, NV);
         case EPI_GATEUP:

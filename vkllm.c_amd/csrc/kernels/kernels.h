@@ -77,6 +77,7 @@ enum GemvEpi : int
     // am_io->id: each workgroup publishes its best (value, row), the last to arrive on am_count reduces them and
     // clears the counter (no workgroup waits for another)
     EPI_ARGMAX = 4,
+    EPI_RAW = 5, // EPI_PLAIN's out from the input as given, no RMSNorm (the MATMUL op's mat_mul_vec case)
 };
 
 struct GemvArgs

@@ -336,6 +336,75 @@ __global__ void rope_kernel(TView in, TView out, uint32_t offset, RopeFreqs fr, 
     }
 }
 
+// fp16 views whose rows (the W axis) are contiguous and 16-byte aligned, the layout of both the isolated operator and
+// the model's permuted Q/K views: one workgroup per (position h, batch b) computes the row's cos/sin pairs once into
+// LDS, then rotates 16-byte vectors of every channel with them. Each pair's angle and its cosf/sinf are those of
+// rope_kernel, and so are the products, so the outputs are identical.
+__global__ __launch_bounds__(256) void rope_rows_kernel(TView in, TView out, uint32_t offset, RopeFreqs fr, int neox)
+{
+    __shared__ float cs[2 * kMaxRopeFreqs];
+    const uint32_t h = blockIdx.x, b = blockIdx.y;
+    const uint32_t half = in.n[3] / 2, C = in.n[1];
+    for (uint32_t w = threadIdx.x; w < half; w += blockDim.x)
+    {
+        const float f = (float)(offset + h) / fr.f[w];
+        cs[2 * w] = cosf(f);
+        cs[2 * w + 1] = sinf(f);
+    }
+    __syncthreads();
+    const uint16_t *src = (const uint16_t *)in.p;
+    uint16_t *dst = (uint16_t *)out.p;
+    if (!neox)
+    {
+        // a vector holds 4 adjacent pairs (2w, 2w + 1)
+        const uint32_t nv = in.n[3] / 8;
+        for (uint32_t i = threadIdx.x; i < C * nv; i += blockDim.x)
+        {
+            const uint32_t c = i / nv, v = i % nv;
+            const u32x4 x = *(const u32x4 *)(src + voff(in, b, c, h, 8 * v));
+            u32x4 o;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+            {
+                const uint32_t w = 4 * v + k;
+                const float fc = cs[2 * w], fs = cs[2 * w + 1];
+                const float v0 = half_lo(x[k]), v1 = half_hi(x[k]);
+                o[k] = pack2(f2h(fc * v0 - fs * v1), f2h(fs * v0 + fc * v1));
+            }
+            *(u32x4 *)(dst + voff(out, b, c, h, 8 * v)) = o;
+        }
+    }
+    else
+    {
+        // pairs (w, w + half): a vector of the low half with the matching vector of the high half, 8 pairs
+        const uint32_t nv = half / 8;
+        for (uint32_t i = threadIdx.x; i < C * nv; i += blockDim.x)
+        {
+            const uint32_t c = i / nv, v = i % nv;
+            const u32x4 lo = *(const u32x4 *)(src + voff(in, b, c, h, 8 * v));
+            const u32x4 hi = *(const u32x4 *)(src + voff(in, b, c, h, half + 8 * v));
+            u32x4 olo, ohi;
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+            {
+                const uint32_t w0 = 8 * v + 2 * k, w1 = w0 + 1;
+                const float a0 = half_lo(lo[k]), b0 = half_lo(hi[k]), a1 = half_hi(lo[k]), b1 = half_hi(hi[k]);
+                olo[k] = pack2(f2h(cs[2 * w0] * a0 - cs[2 * w0 + 1] * b0), f2h(cs[2 * w1] * a1 - cs[2 * w1 + 1] * b1));
+                ohi[k] = pack2(f2h(cs[2 * w0 + 1] * a0 + cs[2 * w0] * b0), f2h(cs[2 * w1 + 1] * a1 + cs[2 * w1] * b1));
+            }
+            *(u32x4 *)(dst + voff(out, b, c, h, 8 * v)) = olo;
+            *(u32x4 *)(dst + voff(out, b, c, h, half + 8 * v)) = ohi;
+        }
+    }
+}
+
+static bool rope_rows_ok(const TView &t, bool neox)
+{
+    const uint32_t W = t.n[3];
+    return t.dt == DT_F16 && t.s[3] == 1 && (neox ? (W / 2) % 8 == 0 : W % 8 == 0) && t.s[2] % 8 == 0 &&
+           t.s[1] % 8 == 0 && t.s[0] % 8 == 0 && (uintptr_t)t.p % 16 == 0 && t.n[0] <= 65535;
+}
+
 hipError_t launch_rope(hipStream_t st, const TView &in, const TView &out, uint32_t offset, const float *freqs_host,
                        bool neox)
 {
@@ -348,6 +417,11 @@ hipError_t launch_rope(hipStream_t st, const TView &in, const TView &out, uint32
     uint64_t total = (uint64_t)in.n[0] * in.n[1] * in.n[2] * half;
     if (total == 0)
         return hipSuccess;
+    if (rope_rows_ok(in, neox) && rope_rows_ok(out, neox))
+    {
+        rope_rows_kernel<<<dim3(in.n[2], in.n[0]), 256, 0, st>>>(in, out, offset, fr, neox ? 1 : 0);
+        return hipGetLastError();
+    }
     uint32_t grid = blocks_for(total, 256);
     grid = grid > 65536 ? 65536 : grid;
     rope_kernel<<<grid, 256, 0, st>>>(in, out, offset, fr, neox ? 1 : 0, total);

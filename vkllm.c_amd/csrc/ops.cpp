@@ -313,7 +313,7 @@ static hipError_t launch_op_gemv(vkllm_context *ctx, const vk::TView &a, const v
     g.rows = out.n[3];
     g.units = (g.rows + 1) / 2;
     g.out = (uint16_t *)out.p;
-    return vk::launch_gemv(ctx->device->stream, vk::EPI_PLAIN, g, ctx->device->cu_count);
+    return vk::launch_gemv(ctx->device->stream, vk::EPI_RAW, g, ctx->device->cu_count);
 }
 
 // 64 MB of split-K partials for the op's tile GEMM, made once per context (the kernels then split K only as far as
