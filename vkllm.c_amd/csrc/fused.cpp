@@ -27,6 +27,7 @@ struct FusedPlan
     vkllm_tensor *input_toks;
     uint32_t offset;
     uint32_t S;
+    bool ran = false; // fused_plan_run enqueued (and completed) the step
 };
 
 // Short-cache decode steps are captured per bucket of kSmallBucket cache positions: a bucket's launches bound their
@@ -43,7 +44,31 @@ struct FusedState
     vk::Step *step = nullptr;    // device
     vk::Step *step_h = nullptr;  // pinned staging for step + first token
     uint32_t *io_h = nullptr;    // pinned: a prefill's ids, uploaded and read back
-    vk::DecodeIo *dio = nullptr; // pinned, coherent: a single-token step's position, token and arg-max id
+    // single-token steps alternate between two slots, so that the next step can be enqueued while the host still
+    // reads this one (launch-ahead, below). Each slot has a pinned coherent DecodeIo (position, token, arg-max id),
+    // a device copy of its arg-max id, a logits row and its own captured graphs; `dio` and `slot` name the slot
+    // being enqueued
+    vk::DecodeIo *dio_slots = nullptr; // [2]
+    vk::DecodeIo *dio = nullptr;
+    uint32_t *slot_ids = nullptr;      // [2], device
+    uint16_t *slot_logits = nullptr;   // [2][V], device
+    int slot = 0;
+    hipEvent_t slot_done[2] = {};      // recorded after each slot's last launch
+    // Launch-ahead (VKLLM_LAUNCH_AHEAD=0: off). After enqueueing a single-token step at position p, the step at p + 1
+    // is enqueued behind it with the first step's device-side arg max as its token, before the host has read that id.
+    // The reference driver's loop feeds exactly that id back at p + 1 (tests/vkllm_test_infer_gguf.c:255-269), so its
+    // next graph_run finds the step already queued or done and only waits. Any other next call (another token or
+    // position, a prompt step, timing) discards the step launched ahead, whose only lasting effect is the cache rows
+    // of position p + 1: a step at that position rewrites them before reading them, and no step reads a row past its
+    // own position.
+    bool ahead_enabled = true;
+    bool ahead_live = false;
+    int ahead_slot = 0;
+    uint32_t ahead_offset = 0, ahead_token = 0; // the step launched ahead: its position, and its token once known
+    // the last completed single-token step (what vkllm_hip_model_last_logits and the timing replays refer to)
+    int done_slot = 0;
+    uint32_t done_offset = 0, done_token = 0;
+    const uint16_t *last_logits = nullptr; // logits of the last completed step (a slot's row, or the prompt's rows)
     float *freqs = nullptr;      // device copy of the RoPE denominators
     // decode attention scratch: scores [H, ctx], chunk statistics [H, cmax, 2], chunk partial sums [H, cmax, hd]
     float *att_scores = nullptr, *att_stats = nullptr, *att_part = nullptr;
@@ -88,11 +113,11 @@ struct FusedState
     // captured single-token steps, one per attention variant: [b] (b < kSmallBuckets) the one-kernel attention for
     // caches of at most (b + 1) * kSmallBucket positions (the launch's bound for its LDS and speculative loads),
     // [kSmallBuckets] the long-cache attention
-    hipGraph_t graph[kSmallBuckets + 1] = {};
-    hipGraphExec_t exec[kSmallBuckets + 1] = {};
+    hipGraph_t graph[2][kSmallBuckets + 1] = {};
+    hipGraphExec_t exec[2][kSmallBuckets + 1] = {};
     // the positions bound of the short-cache launches being enqueued (the current variant's)
     uint32_t small_kv_max = 0;
-    int last_exec = -1;
+    int last_exec = -1, last_exec_slot = 0;
     // timing mode: one record per graph node a fused launch computes (per layer, then the step's own nodes), named
     // as the node; after a timed step the graph's nodes point at the records that received launches
     std::vector<vkllm_pipeline> node_pipes;
@@ -180,6 +205,11 @@ void *fused_plan_new(vkllm_models_llama2 *model, vkllm_tensor *input_toks, uint3
     return p;
 }
 
+bool fused_plan_ran(const void *plan)
+{
+    return ((const FusedPlan *)plan)->ran;
+}
+
 void fused_plan_free(void *plan)
 {
     delete (FusedPlan *)plan;
@@ -213,15 +243,16 @@ static void free_buffers(FusedState *fs)
 
 static void drop_graphs(FusedState *fs)
 {
-    for (uint32_t i = 0; i <= kSmallBuckets; ++i)
-    {
-        if (fs->exec[i])
-            (void)hipGraphExecDestroy(fs->exec[i]);
-        if (fs->graph[i])
-            (void)hipGraphDestroy(fs->graph[i]);
-        fs->exec[i] = nullptr;
-        fs->graph[i] = nullptr;
-    }
+    for (int k = 0; k < 2; ++k)
+        for (uint32_t i = 0; i <= kSmallBuckets; ++i)
+        {
+            if (fs->exec[k][i])
+                (void)hipGraphExecDestroy(fs->exec[k][i]);
+            if (fs->graph[k][i])
+                (void)hipGraphDestroy(fs->graph[k][i]);
+            fs->exec[k][i] = nullptr;
+            fs->graph[k][i] = nullptr;
+        }
     fs->last_exec = -1;
 }
 
@@ -252,8 +283,15 @@ void fused_model_release(vkllm_context *ctx, vkllm_models_llama2 *model)
         (void)hipHostFree(fs->step_h);
     if (fs->io_h)
         (void)hipHostFree(fs->io_h);
-    if (fs->dio)
-        (void)hipHostFree(fs->dio);
+    if (fs->dio_slots)
+        (void)hipHostFree(fs->dio_slots);
+    if (fs->slot_ids)
+        (void)hipFree(fs->slot_ids);
+    if (fs->slot_logits)
+        (void)hipFree(fs->slot_logits);
+    for (hipEvent_t e : fs->slot_done)
+        if (e)
+            (void)hipEventDestroy(e);
     delete fs;
     mp->fs = nullptr;
 }
@@ -331,8 +369,16 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         HIP_TRY(hipMalloc(&fs->step, sizeof(vk::Step)));
         HIP_TRY(hipHostMalloc((void **)&fs->step_h, sizeof(vk::Step), hipHostMallocDefault));
         // read and written by the decode kernels in place: coherent, so no GPU cache holds a stale copy
-        HIP_TRY(hipHostMalloc((void **)&fs->dio, sizeof(vk::DecodeIo), hipHostMallocCoherent));
-        memset(fs->dio, 0, sizeof(vk::DecodeIo));
+        HIP_TRY(hipHostMalloc((void **)&fs->dio_slots, 2 * sizeof(vk::DecodeIo), hipHostMallocCoherent));
+        memset(fs->dio_slots, 0, 2 * sizeof(vk::DecodeIo));
+        fs->dio = fs->dio_slots;
+        HIP_TRY(hipMalloc(&fs->slot_ids, 2 * sizeof(uint32_t)));
+        HIP_TRY(hipMemset(fs->slot_ids, 0, 2 * sizeof(uint32_t)));
+        HIP_TRY(hipMalloc(&fs->slot_logits, (size_t)2 * mp->V * 2));
+        for (hipEvent_t &e : fs->slot_done)
+            HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+        const char *la = getenv("VKLLM_LAUNCH_AHEAD");
+        fs->ahead_enabled = !(la && *la == '0');
         HIP_TRY(hipMalloc(&fs->freqs, sizeof(float) * (mp->hd / 2 + 1)));
         HIP_TRY(hipMemcpyAsync(fs->freqs, mp->rope_freqs.data(), sizeof(float) * mp->hd / 2, hipMemcpyHostToDevice,
                                ctx->device->stream));
@@ -391,6 +437,8 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         return VKLLM_ERR_OK;
     // growing the activation buffers moves them: the captured decode graphs refer to the old ones
     HIP_TRY(hipStreamSynchronize(ctx->device->stream));
+    fs->ahead_live = false;
+    fs->last_logits = nullptr;
     drop_graphs(fs);
     free_buffers(fs);
     if (fs->io_h)
@@ -440,7 +488,7 @@ static hipError_t launch_decode_kernel(vkllm_context *ctx, ModelPriv *mp, Kernel
     {
     case KID_F_EMBED:
         return vk::launch_embed_decode(st, fs->dio, fs->step, mp->embd, resid_out ? resid_out : fs->h, V, D,
-                                       mp->pad_id);
+                                       mp->pad_id, fs->slot_ids + (1 - fs->slot));
     case KID_F_QKV:
         // RMSNorm(h) -> [Wq;Wk;Wv] -> RoPE(q, k); q to fs->q, k and v into the caches at the step's position
         g.x = fs->h;
@@ -527,11 +575,11 @@ static hipError_t launch_decode_kernel(vkllm_context *ctx, ModelPriv *mp, Kernel
         g.w = mp->out_w;
         g.rows = V;
         g.units = (V + 1) / 2;
-        g.out = fs->logits;
+        g.out = fs->slot_logits + (size_t)fs->slot * V;
         if (!fs->argmax_epi)
             return vk::launch_gemv(st, vk::EPI_PLAIN, g, cu);
         // the logits and their arg max (what KID_F_ARGMAX computes) in one launch
-        g.am_ids = fs->ids;
+        g.am_ids = fs->slot_ids + fs->slot;
         g.am_io = fs->dio;
         g.am_val = fs->am_val;
         g.am_idx = fs->am_idx;
@@ -539,7 +587,8 @@ static hipError_t launch_decode_kernel(vkllm_context *ctx, ModelPriv *mp, Kernel
         g.am_cap = kArgmaxCandidates;
         return vk::launch_gemv(st, vk::EPI_ARGMAX, g, cu);
     case KID_F_ARGMAX:
-        return vk::launch_argmax_rows(st, fs->logits, fs->ids, 1, V, fs->dio);
+        return vk::launch_argmax_rows(st, fs->slot_logits + (size_t)fs->slot * V, fs->slot_ids + fs->slot, 1, V,
+                                      fs->dio);
     default:
         return hipErrorInvalidValue;
     }
@@ -798,6 +847,36 @@ vkllm_err_t fused_plan_init(vkllm_context *ctx, vkllm_graph *graph)
     return ensure_state(ctx, mp, p->S);
 }
 
+// the slot whose DecodeIo, logits row and arg-max id the decode launches being enqueued use
+static void select_slot(FusedState *fs, int k)
+{
+    fs->slot = k;
+    fs->dio = fs->dio_slots + k;
+}
+
+// Drops a step launched ahead (after it finished) and points the decode launches at the last completed step's
+// slot and inputs: for work on the stream that must not be mistaken for, or run with, that step.
+static vkllm_err_t discard_ahead(vkllm_context *ctx, FusedState *fs)
+{
+    HIP_TRY(hipStreamSynchronize(ctx->device->stream));
+    fs->ahead_live = false;
+    select_slot(fs, fs->done_slot);
+    fs->dio->offset = fs->done_offset;
+    fs->dio->token = fs->done_token;
+    fs->dio->token_dev = 0;
+    fs->dio->err = 0;
+    return VKLLM_ERR_OK;
+}
+
+vkllm_err_t fused_plan_discard_ahead(vkllm_context *ctx, vkllm_graph *graph)
+{
+    auto *p = (FusedPlan *)graph->plan;
+    ModelPriv *mp = p ? model_priv(p->model) : nullptr;
+    if (!mp || !mp->fs)
+        return VKLLM_ERR_OK;
+    return discard_ahead(ctx, mp->fs);
+}
+
 // Enqueues one single-token step: a replay of the captured graph for this attention variant (captured on first
 // use), or direct launches when graph replay or timing says so.
 static vkllm_err_t launch_decode_step(vkllm_context *ctx, ModelPriv *mp, uint32_t v)
@@ -806,7 +885,8 @@ static vkllm_err_t launch_decode_step(vkllm_context *ctx, ModelPriv *mp, uint32_
     hipStream_t st = ctx->device->stream;
     if (!ctx->device->graph_replay || ctx->device->timing)
         return enqueue_decode(ctx, mp, v);
-    if (!fs->exec[v])
+    const int k = fs->slot;
+    if (!fs->exec[k][v])
     {
         HIP_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeRelaxed));
         vkllm_err_t rc = enqueue_decode(ctx, mp, v);
@@ -819,11 +899,12 @@ static vkllm_err_t launch_decode_step(vkllm_context *ctx, ModelPriv *mp, uint32_
             return rc;
         }
         HIP_TRY(ce);
-        fs->graph[v] = g;
-        HIP_TRY(hipGraphInstantiate(&fs->exec[v], g, nullptr, nullptr, 0));
+        fs->graph[k][v] = g;
+        HIP_TRY(hipGraphInstantiate(&fs->exec[k][v], g, nullptr, nullptr, 0));
     }
-    HIP_TRY(hipGraphLaunch(fs->exec[v], st));
+    HIP_TRY(hipGraphLaunch(fs->exec[k][v], st));
     fs->last_exec = v;
+    fs->last_exec_slot = k;
     return VKLLM_ERR_OK;
 }
 
@@ -870,38 +951,80 @@ vkllm_err_t fused_plan_run(vkllm_context *ctx, vkllm_graph *graph)
     vkllm_tensor *out = graph->output_node;
     if (S == 1)
     {
-        // position and token go through the pinned block that the step's first kernel reads; the arg max writes
-        // the chosen id back into it
-        fs->dio->offset = p->offset;
-        fs->dio->token = toks[0];
-        fs->dio->err = 0;
+        // position and token go through the slot's pinned block that the step's first kernel reads; the arg max
+        // writes the chosen id back into it
         const uint64_t t0 = fs->trace ? host_ns() : 0;
+        const bool direct = !ctx->device->graph_replay || ctx->device->timing;
         const uint32_t variant = decode_variant(fs, p->offset + 1);
-        _CHECK(launch_decode_step(ctx, mp, variant));
+        int slot;
+        if (fs->ahead_live && !direct && fs->ahead_offset == p->offset && fs->ahead_token == toks[0])
+            slot = fs->ahead_slot; // launched ahead with this very token at this position: queued or done
+        else
+        {
+            // a step launched ahead for another token or position runs before this one (stream order); this step
+            // rewrites the cache rows it wrote, or never reads them
+            slot = fs->ahead_live ? 1 - fs->ahead_slot : 1 - fs->done_slot;
+            select_slot(fs, slot);
+            fs->dio->offset = p->offset;
+            fs->dio->token = toks[0];
+            fs->dio->token_dev = 0;
+            fs->dio->err = 0;
+            _CHECK(launch_decode_step(ctx, mp, variant));
+            HIP_TRY(hipEventRecord(fs->slot_done[slot], st));
+        }
+        fs->ahead_live = false;
+        if (fs->ahead_enabled && !direct && p->offset + 1 < mp->ctx)
+        {
+            // the step at p + 1 behind this one, its token this step's device-side arg max
+            const int nx = 1 - slot;
+            select_slot(fs, nx);
+            fs->dio->offset = p->offset + 1;
+            fs->dio->token = 0;
+            fs->dio->token_dev = 1;
+            fs->dio->err = 0;
+            _CHECK(launch_decode_step(ctx, mp, decode_variant(fs, p->offset + 2)));
+            HIP_TRY(hipEventRecord(fs->slot_done[nx], st));
+            fs->ahead_live = true;
+            fs->ahead_slot = nx;
+            fs->ahead_offset = p->offset + 1;
+        }
+        select_slot(fs, slot);
         const uint64_t t1 = fs->trace ? host_ns() : 0;
-        HIP_TRY(hipStreamSynchronize(st));
+        HIP_TRY(hipEventSynchronize(fs->slot_done[slot]));
         if (((volatile vk::DecodeIo *)fs->dio)->err)
         {
             // A bounded wait between workgroups gave up (the GPU is shared or busy, so not every block of the launch
-            // was resident). Clear the counters that launch left, switch to the attention kernels that never wait,
-            // and run the step again: it starts from the embedding and rewrites the same cache rows, so a second run
-            // gives the step's result.
+            // was resident). Let the step launched ahead finish and drop it, clear the counters the launches left,
+            // switch to the attention kernels that never wait, and run the step again: it starts from the
+            // embedding and rewrites the same cache rows, so a second run gives the step's result.
             log_error("decode step at position %u: a kernel's wait for other workgroups gave up; running it again "
                       "with attention kernels that do not wait",
                       p->offset);
+            HIP_TRY(hipStreamSynchronize(st));
+            fs->ahead_live = false;
             HIP_TRY(hipMemsetAsync(fs->attn_sync, 0, vk::kAttnSyncWords * sizeof(uint32_t), st));
             HIP_TRY(hipMemsetAsync(fs->att_long_sync, 0, (size_t)mp->H * vk::kAttnLongStride * sizeof(uint32_t), st));
             HIP_TRY(hipMemsetAsync(fs->att_count, 0, (size_t)mp->H * sizeof(uint32_t), st));
             drop_graphs(fs);
             fs->attn_long = false;
             fs->attn_o = false;
+            fs->dio->offset = p->offset;
+            fs->dio->token = toks[0];
+            fs->dio->token_dev = 0;
             fs->dio->err = 0;
             _CHECK(launch_decode_step(ctx, mp, variant));
             HIP_TRY(hipStreamSynchronize(st));
             if (((volatile vk::DecodeIo *)fs->dio)->err)
                 return VKLLM_ERR_VULKAN;
         }
-        fs->io_h[0] = ((volatile vk::DecodeIo *)fs->dio)->id;
+        const uint32_t id = ((volatile vk::DecodeIo *)fs->dio)->id;
+        fs->io_h[0] = id;
+        if (fs->ahead_live)
+            fs->ahead_token = id;
+        fs->done_slot = slot;
+        fs->done_offset = p->offset;
+        fs->done_token = toks[0];
+        fs->last_logits = fs->slot_logits + (size_t)slot * mp->V;
         if (fs->trace)
         {
             fs->trace_steps += 1;
@@ -911,6 +1034,7 @@ vkllm_err_t fused_plan_run(vkllm_context *ctx, vkllm_graph *graph)
     }
     else
     {
+        fs->ahead_live = false; // a step launched ahead runs first (stream order); nothing reads what it wrote
         fs->step_h->offset = p->offset;
         fs->step_h->S = S;
         memcpy(fs->io_h, toks, (size_t)S * 4);
@@ -919,7 +1043,9 @@ vkllm_err_t fused_plan_run(vkllm_context *ctx, vkllm_graph *graph)
         _CHECK(enqueue_prefill(ctx, mp, S, p->offset));
         HIP_TRY(hipMemcpyAsync(fs->io_h, fs->ids, (size_t)S * 4, hipMemcpyDeviceToHost, st));
         HIP_TRY(hipStreamSynchronize(st));
+        fs->last_logits = fs->logits;
     }
+    p->ran = true;
     // results: the arg-max ids into the output node, as the reference's mapped ARG_MAX output holds them
     if (out->data.host)
     {
@@ -931,7 +1057,8 @@ vkllm_err_t fused_plan_run(vkllm_context *ctx, vkllm_graph *graph)
     void *out_dev = tensor_dev(ctx, out);
     if (!out_dev)
         return VKLLM_ERR_ALLOC;
-    HIP_TRY(hipMemcpyAsync(out_dev, fs->ids, (size_t)S * 4, hipMemcpyDeviceToDevice, st));
+    HIP_TRY(hipMemcpyAsync(out_dev, S == 1 ? fs->slot_ids + fs->done_slot : fs->ids, (size_t)S * 4,
+                           hipMemcpyDeviceToDevice, st));
     HIP_TRY(hipStreamSynchronize(st));
     out->data.valid = true;
     return attach_node_costs(ctx, fs, graph);
@@ -947,8 +1074,10 @@ extern "C" vkllm_err_t vkllm_hip_model_last_logits(struct vkllm_context *ctx, st
     _CHECK_ARGS(ctx && model && dst);
     ModelPriv *mp = model_priv(model);
     _CHECK_ARGS(mp && mp->fs && mp->fs->logits && rows <= mp->fs->cap_S);
-    HIP_TRY(hipMemcpyAsync(dst, mp->fs->logits, (size_t)rows * mp->V * 2, hipMemcpyDeviceToHost,
-                           ctx->device->stream));
+    // a single-token step's logits are in its slot's row (a step launched ahead writes the other slot's)
+    const uint16_t *src = mp->fs->last_logits ? mp->fs->last_logits : mp->fs->logits;
+    _CHECK_ARGS(src == mp->fs->logits || rows == 1);
+    HIP_TRY(hipMemcpyAsync(dst, src, (size_t)rows * mp->V * 2, hipMemcpyDeviceToHost, ctx->device->stream));
     HIP_TRY(hipStreamSynchronize(ctx->device->stream));
     return VKLLM_ERR_OK;
 }
@@ -972,13 +1101,17 @@ extern "C" vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *ctx, st
                     {"fused_o_resid", KID_F_O_RESID},     {"fused_gateup", KID_F_GATEUP},
                     {"fused_down_resid", KID_F_DOWN_RESID}, {"fused_logits", KID_F_LOGITS},
                     {"fused_argmax", KID_F_ARGMAX}};
+    // the launches below recompute the last completed step (same token, same position): a step launched ahead is
+    // dropped first, so that nothing is mistaken for it
+    _CHECK(discard_ahead(ctx, fs));
     const bool whole = strcmp(family, "decode_step") == 0;
     int kid = -1;
     for (const auto &f : families)
         if (strcmp(family, f.name) == 0)
             kid = f.kid;
     _CHECK_ARGS(whole || kid >= 0);
-    if (whole && fs->last_exec < 0)
+    const int replay = (int)decode_variant(fs, fs->done_offset + 1);
+    if (whole && (fs->last_exec < 0 || !fs->exec[fs->done_slot][replay]))
     {
         log_error("decode_step timing needs a captured decode step (graph replay on, one single-token step run)");
         return VKLLM_ERR_ARGS;
@@ -1000,7 +1133,7 @@ extern "C" vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *ctx, st
     // the residual GEMVs write into fs->xn (a scratch row) so that repeating them leaves the model state unchanged
     auto launch = [&](uint32_t r) -> hipError_t {
         if (whole)
-            return hipGraphLaunch(fs->exec[fs->last_exec], st);
+            return hipGraphLaunch(fs->exec[fs->done_slot][replay], st);
         return launch_decode_kernel(ctx, mp, (KernelId)kid, r % mp->L, fs->xn);
     };
     // one untimed launch so the first timed one does not pay for code loading

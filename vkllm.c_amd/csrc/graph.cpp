@@ -115,6 +115,8 @@ extern "C" vkllm_err_t vkllm_graph_run(struct vkllm_context *context, struct vkl
     _CHECK_ARGS(context && graph && graph->output_node && graph->commands);
     if (use_fused(context, graph))
         return fused_plan_run(context, graph);
+    if (graph->plan) // node by node over a model whose fused steps may have launched one ahead
+        _CHECK(fused_plan_discard_ahead(context, graph));
     _CHECK(vkllm_commands_begin(context, graph->commands));
     vkllm_err_t rc =
         visit_post_order(graph->output_node, [&](vkllm_tensor *t) { return op_run(context, graph->commands, t); });
@@ -139,8 +141,10 @@ extern "C" vkllm_err_t vkllm_graph_free(struct vkllm_context *context, struct vk
 {
     DeviceScope device_scope(context);
     _CHECK_ARGS(context && graph);
-    // queued work may still read these tensors
-    (void)hipStreamSynchronize(context->device->stream);
+    // queued node kernels may still read these tensors. A fused step's kernels read none of them (only the model's
+    // buffers), so after one the next step, if it was launched ahead, keeps running while the graph is freed.
+    if (!(graph->plan && fused_plan_ran(graph->plan)))
+        (void)hipStreamSynchronize(context->device->stream);
     for (size_t i = 0; i < graph->nodes->used_n; ++i)
         vkllm_tensor_free(context, graph->nodes->data[i]);
     vkllm_array_tensor_free(graph->nodes);

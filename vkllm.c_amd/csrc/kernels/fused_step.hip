@@ -51,10 +51,10 @@ hipError_t launch_embed_rows(hipStream_t st, const uint32_t *toks, uint32_t S, c
 
 // first kernel of a single-token step: position and token from the pinned host block
 __global__ void embed_decode_kernel(const DecodeIo *io, Step *step, const uint16_t *embd, uint16_t *h, uint32_t V,
-                                    uint32_t D, uint32_t unk)
+                                    uint32_t D, uint32_t unk, const uint32_t *prev_id)
 {
     const uint32_t offset = io->offset;
-    uint32_t tok = io->token;
+    uint32_t tok = io->token_dev ? *prev_id : io->token;
     if (threadIdx.x == 0)
     {
         step->offset = offset;
@@ -76,11 +76,11 @@ __global__ void embed_decode_kernel(const DecodeIo *io, Step *step, const uint16
 }
 
 hipError_t launch_embed_decode(hipStream_t st, const DecodeIo *io, Step *step, const uint16_t *embd, uint16_t *h,
-                               uint32_t V, uint32_t D, uint32_t unk)
+                               uint32_t V, uint32_t D, uint32_t unk, const uint32_t *prev_id)
 {
-    if (D % 8 != 0)
+    if (D % 8 != 0 || !prev_id)
         return hipErrorInvalidValue;
-    embed_decode_kernel<<<1, 256, 0, st>>>(io, step, embd, h, V, D, unk);
+    embed_decode_kernel<<<1, 256, 0, st>>>(io, step, embd, h, V, D, unk, prev_id);
     return hipGetLastError();
 }
 

@@ -55,11 +55,13 @@ struct DecodeIo
     uint32_t offset;
     uint32_t token;
     uint32_t id;
-    uint32_t err; // nonzero when a kernel's bounded wait gave up during the step
+    uint32_t err;       // nonzero when a kernel's bounded wait gave up during the step
+    uint32_t token_dev; // nonzero: the step's token is the device-side arg max of the step before (launch-ahead)
 };
-// single-token step: step = {io->offset, 1}, h = embd[io->token] (ids >= V read row unk)
+// single-token step: step = {io->offset, 1}, h = embd[token] (ids >= V read row unk), where token is io->token, or
+// *prev_id when io->token_dev is set
 hipError_t launch_embed_decode(hipStream_t st, const DecodeIo *io, Step *step, const uint16_t *embd, uint16_t *h,
-                               uint32_t V, uint32_t D, uint32_t unk);
+                               uint32_t V, uint32_t D, uint32_t unk, const uint32_t *prev_id);
 // h[s] = embd[toks[s]] (ids >= V read row unk), s < S; D % 8 == 0
 hipError_t launch_embed_rows(hipStream_t st, const uint32_t *toks, uint32_t S, const uint16_t *embd, uint16_t *h,
                              uint32_t V, uint32_t D, uint32_t unk);

@@ -193,4 +193,8 @@ void *fused_plan_new(vkllm_models_llama2 *model, vkllm_tensor *input_toks, uint3
 void fused_plan_free(void *plan);
 vkllm_err_t fused_plan_init(vkllm_context *ctx, vkllm_graph *graph);
 vkllm_err_t fused_plan_run(vkllm_context *ctx, vkllm_graph *graph);
+// true once the plan ran as fused kernels (which read none of the graph's node tensors)
+bool fused_plan_ran(const void *plan);
+// drops a single-token step launched ahead for the plan's model (before node-by-node execution of its graph)
+vkllm_err_t fused_plan_discard_ahead(vkllm_context *ctx, vkllm_graph *graph);
 void fused_model_release(vkllm_context *ctx, vkllm_models_llama2 *model);

@@ -231,9 +231,15 @@ extern "C" vkllm_err_t vkllm_tensor_invalid_cache(struct vkllm_context *context,
     void *dev = tensor_dev(context, b);
     if (!dev)
         return VKLLM_ERR_ALLOC;
+    // the host mirror is brought up to date only when the device holds newer contents; a mirror that is current (a
+    // fused step writes its arg-max ids there once they are final) needs no wait, so work queued behind it (a step
+    // launched ahead) keeps running while the caller reads
     if (b->data.valid && !b->data.host_current)
+    {
         HIP_TRY(hipMemcpyAsync(b->data.host, dev, b->bytes, hipMemcpyDeviceToHost, context->device->stream));
-    HIP_TRY(hipStreamSynchronize(context->device->stream));
+        HIP_TRY(hipStreamSynchronize(context->device->stream));
+        b->data.host_current = true;
+    }
     return VKLLM_ERR_OK;
 }
 
