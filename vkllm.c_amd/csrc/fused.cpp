@@ -100,6 +100,13 @@ struct FusedState
     // one-kernel attention and the output projection in one launch (VKLLM_ATTN_O=1; the default is two launches,
     // which measure faster at the 7B widths); cleared when the device cannot hold both parts' workgroups at once
     bool attn_o = false;
+    // short caches of at most kAttnTailMaxKv positions: each head's attention at the end of the QKV product, by the
+    // workgroup that completes the head's rows (VKLLM_QKV_ATTN=1; the default is the separate attention kernel,
+    // which measures faster at the 7B widths: every head completes in the product's last round, so the attention's
+    // latency follows the product in one 256-thread workgroup per head). head_count: the product's per-head unit
+    // counts, zero between launches.
+    bool qkv_attn = false, qkv_attn_now = false;
+    uint32_t *head_count = nullptr;
     // long caches in one attention kernel (VKLLM_ATTN_LONG=0: two); cleared when the device cannot hold every chunk
     // block at once
     bool attn_long = true;
@@ -275,7 +282,7 @@ void fused_model_release(vkllm_context *ctx, vkllm_models_llama2 *model)
         (void)hipFree(fs->freqs);
     free_stream_tiles(fs);
     void *att[] = {fs->att_scores, fs->att_stats, fs->att_part, fs->att_count, fs->attn_sync, fs->att_long_sync,
-                   fs->gemm_work,  fs->am_val,    fs->am_idx,   fs->am_count};
+                   fs->gemm_work,  fs->am_val,    fs->am_idx,   fs->am_count,  fs->head_count};
     for (void *b : att)
         if (b)
             (void)hipFree(b);
@@ -403,6 +410,11 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         fs->attn_small_max = small < mp->ctx ? small : mp->ctx;
         const char *ao = getenv("VKLLM_ATTN_O");
         fs->attn_o = ao && *ao == '1';
+        const char *qa = getenv("VKLLM_QKV_ATTN");
+        fs->qkv_attn = qa && *qa == '1' && mp->H <= vk::kAttnTailMaxHeads && mp->hd % 8 == 0 &&
+                       mp->hd >= 32 && 64 % (mp->hd / 8) == 0;
+        HIP_TRY(hipMalloc(&fs->head_count, (size_t)mp->H * sizeof(uint32_t)));
+        HIP_TRY(hipMemset(fs->head_count, 0, (size_t)mp->H * sizeof(uint32_t)));
         const char *al = getenv("VKLLM_ATTN_LONG");
         fs->attn_long = !(al && *al == '0');
         const char *re = getenv("VKLLM_ROPE_EPI");
@@ -504,6 +516,16 @@ static hipError_t launch_decode_kernel(vkllm_context *ctx, ModelPriv *mp, Kernel
         g.D = D;
         g.hd = hd;
         g.ctx = mp->ctx;
+        if (fs->qkv_attn_now)
+        {
+            // and each head's attention by the workgroup that completes the head's rows
+            g.attn_out = fs->attn;
+            g.head_count = fs->head_count;
+            g.H = mp->H;
+            g.attn_scale = 1.0f / sqrtf((float)hd);
+            g.attn_err = &fs->dio->err;
+            return vk::launch_gemv(st, vk::EPI_QKV_ATTN, g, cu);
+        }
         return vk::launch_gemv(st, vk::EPI_QKV, g, cu);
     case KID_F_ATTN_SCORES:
     case KID_F_ATTN_PV:
@@ -649,10 +671,20 @@ static vkllm_err_t enqueue_decode(vkllm_context *ctx, ModelPriv *mp, uint32_t va
         const uint32_t end = (variant + 1) * kSmallBucket;
         mp->fs->small_kv_max = end < mp->fs->attn_small_max ? end : mp->fs->attn_small_max;
     }
+    // caches of at most kAttnTailMaxKv positions (this bucket's end): the attention in the QKV product's launch
+    const bool tail_attn = small_attn && mp->fs->qkv_attn && mp->fs->small_kv_max <= vk::kAttnTailMaxKv;
+    mp->fs->qkv_attn_now = tail_attn;
     DTRY(ctx, mp, KID_F_EMBED, 0);
     for (uint32_t l = 0; l < mp->L; ++l)
     {
         DTRY(ctx, mp, KID_F_QKV, l);
+        if (tail_attn)
+        {
+            DTRY(ctx, mp, KID_F_O_RESID, l);
+            DTRY(ctx, mp, KID_F_GATEUP, l);
+            DTRY(ctx, mp, KID_F_DOWN_RESID, l);
+            continue;
+        }
         bool fused_o = false;
         if (small_attn && mp->fs->attn_o)
         {
@@ -1122,12 +1154,15 @@ extern "C" vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *ctx, st
                   fs->dio->offset + 1);
         return VKLLM_ERR_ARGS;
     }
-    if (kid == KID_F_ATTN_SMALL || kid == KID_F_ATTN_O)
     {
         // the launches of the last step's bucket
         const uint32_t b = decode_variant(fs, fs->dio->offset + 1);
-        const uint32_t end = (b + 1) * kSmallBucket;
-        fs->small_kv_max = end < fs->attn_small_max ? end : fs->attn_small_max;
+        if (b < kSmallBuckets)
+        {
+            const uint32_t end = (b + 1) * kSmallBucket;
+            fs->small_kv_max = end < fs->attn_small_max ? end : fs->attn_small_max;
+        }
+        fs->qkv_attn_now = b < kSmallBuckets && fs->qkv_attn && fs->small_kv_max <= vk::kAttnTailMaxKv;
     }
     hipStream_t st = ctx->device->stream;
     // the residual GEMVs write into fs->xn (a scratch row) so that repeating them leaves the model state unchanged

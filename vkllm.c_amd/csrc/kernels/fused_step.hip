@@ -14,6 +14,7 @@
 //   gemv<RESID>    Wd rows, residual add in place
 #include <float.h>
 
+#include "attn_common.h"
 #include "device_common.h"
 #include "kernels.h"
 
@@ -251,6 +252,12 @@ hipError_t launch_gemv_loop(hipStream_t st, int epi, const GemvArgs &a, int cu_c
     return hipGetLastError();
 }
 
+// the QKV product's epilogues (RoPE on q, k; k and v appended to the caches)
+constexpr bool is_qkv(int epi)
+{
+    return epi == EPI_QKV || epi == EPI_QKV_ATTN;
+}
+
 // GEMV with the input prologue overlapped by the weight stream. A wave owns units of R weight rows (R/2 up rows
 // next to R/2 gate rows for EPI_GATEUP; R even for EPI_QKV so RoPE pairs stay together); lane l holds the 16-byte
 // vectors l + 64 i (i < NV) of each row, so NV * 512 >= K. Order of work in a workgroup:
@@ -259,6 +266,7 @@ hipError_t launch_gemv_loop(hipStream_t st, int epi, const GemvArgs &a, int cu_c
 //   3. RMSNorm over the registers (block reduction in LDS), the normalised input into LDS
 //   4. per unit: dot products against LDS, the next unit's weights issued before this unit's reduction
 // Vector-memory counters retire in issue order, so waiting for the input (issued first) never waits for weights.
+// EPI_QKV_ATTN then finishes each head's attention in the workgroup that completes the head's rows.
 template <int EPI> __device__ __forceinline__ void gemv_rows_of(const GemvArgs &a, uint32_t u, int R, uint32_t *rows)
 {
     for (int k = 0; k < R; ++k)
@@ -312,6 +320,20 @@ template <int EPI, int R> __device__ __forceinline__ void gemv_epilogue(const Ge
             const uint32_t region = r0 / a.D, rr = r0 % a.D, head = rr / a.hd, dim = rr % a.hd;
             const float v0 = h2f(f2h(acc[k])), v1 = h2f(f2h(acc[k + 1]));
             const size_t cache = ((size_t)head * a.ctx + pos) * a.hd + dim;
+            if constexpr (EPI == EPI_QKV_ATTN)
+            {
+                // the pair as one agent-scope store, written through to where another XCD's workgroup reads it
+                if (region == 2)
+                {
+                    store_pair<true>(a.vc + cache, v0, v1);
+                    continue;
+                }
+                const float f = (float)pos / fq[k / 2];
+                const float c = cosf(f), sn = sinf(f);
+                store_pair<true>(region == 0 ? a.out + rr : a.kc + cache, rope_mul_sub(c, v0, sn, v1),
+                                 rope_mul_add(sn, v0, c, v1));
+                continue;
+            }
             if (region == 2)
             {
                 a.vc[cache] = f2h(v0);
@@ -425,6 +447,157 @@ __device__ __forceinline__ void gemv_argmax_finish(const GemvArgs &a, float bv, 
     }
 }
 
+// EPI_QKV_ATTN's tail, all 256 threads of the workgroup: single-token attention of head `head` over kv positions
+// (src/models/vkllm_llama2_layers.c:223-257 with src/shaders/vkllm_softmax.comp:42-96), with the reference's rounding
+// points: s_j = fp16(scale q.k_j) (the key layout and sums of the short-cache kernel), M and L over all kv scores,
+// p_j = fp16(exp(s_j - M) / L), out[d] = fp16(sum_j p_j v_j[d]); kv == hd takes the transposed product p . V^T.
+// sm (the input row's LDS, sized for this) holds kAttnTailMaxKv scores followed by 4 * hd partial sums. The caller has acquired the head's rows (q and this
+// position's K and V rows were stored by other workgroups of this launch).
+__device__ void qkv_attention_tail(const GemvArgs &a, uint32_t head, float *sm)
+{
+    constexpr uint32_t NT = 256, NW = NT / 64;
+    constexpr int U = 8, UV = 8;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t hd = a.hd, kv = a.step->offset + 1, vpr = hd / 8;
+    const uint16_t *Kh = a.kc + (size_t)head * a.ctx * hd, *Vh = a.vc + (size_t)head * a.ctx * hd;
+    uint16_t *out = a.attn_out + (size_t)head * hd;
+    // V rows: lane = (vector vl, row slot within the wave); the block covers `slots` rows per pass, the first UV
+    // passes requested before the scores
+    const uint32_t seg = 64 / vpr, vl = lane / seg, rs = wave * seg + lane % seg, slots = NW * seg;
+    const u32x4 *Vv = (const u32x4 *)Vh + vl;
+    const bool transposed = kv == hd;
+    u32x4 vv[UV];
+#pragma unroll
+    for (int t = 0; t < UV; ++t)
+        vv[t] = Vv[(size_t)min(rs + slots * t, kv - 1) * vpr];
+    const KeyLayout k = key_layout<NT>(a.out + (size_t)head * hd, hd);
+    const u32x4 *Kv = (const u32x4 *)Kh;
+    for (uint32_t jb = k.ks; jb < kv; jb += k.kpp * U)
+    {
+        u32x4 ka[U], kb[U];
+        load_keys<U>(k, Kv, jb, kv - 1, ka, kb);
+        score_keys<U>(k, ka, kb, jb, kv, a.attn_scale, sm);
+    }
+    __syncthreads();
+    // softmax statistics, reduced by every wave over all kv scores
+    float M = -FLT_MAX;
+    for (uint32_t j = lane; j < kv; j += 64)
+        M = fmaxf(M, sm[j]);
+    M = wave_max_dpp(M);
+    float L = 0.f;
+    for (uint32_t j = lane; j < kv; j += 64)
+        L += expf(sm[j] - M);
+    L = wave_sum_dpp(L);
+    if (transposed)
+    {
+        __syncthreads(); // every wave has its statistics before the scores become probabilities
+        for (uint32_t j = tid; j < kv; j += NT)
+            sm[j] = h2f(f2h(expf(sm[j] - M) / L));
+        __syncthreads();
+        for (uint32_t r = 2 * tid; r < hd; r += 2 * NT)
+        {
+            const uint16_t *row0 = Vh + (size_t)r * hd, *row1 = row0 + hd;
+            float a0 = 0.f, a1 = 0.f;
+            for (uint32_t j = 0; j < kv; ++j)
+            {
+                a0 = fmaf(sm[j], h2f(row0[j]), a0);
+                a1 = fmaf(sm[j], h2f(row1[j]), a1);
+            }
+            store_pair<false>(out + r, a0, a1);
+        }
+        __syncthreads();
+        return;
+    }
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const uint32_t passes = (kv + slots - 1) / slots;
+    for (uint32_t t0 = 0; t0 < passes; t0 += UV)
+    {
+        if (t0 > 0) // the next UV passes of V rows, all requested at once
+#pragma unroll
+            for (int t = 0; t < UV; ++t)
+                vv[t] = Vv[(size_t)min(rs + slots * (t0 + t), kv - 1) * vpr];
+#pragma unroll
+        for (int t = 0; t < UV; ++t)
+        {
+            const uint32_t j = rs + slots * (t0 + t);
+            const bool live = j < kv;
+            const float pj = live ? h2f(f2h(expf(sm[min(j, kv - 1)] - M) / L)) : 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+            {
+                const uint32_t w = live ? vv[t][e] : 0u;
+                acc[2 * e] = fmaf(pj, half_lo(w), acc[2 * e]);
+                acc[2 * e + 1] = fmaf(pj, half_hi(w), acc[2 * e + 1]);
+            }
+        }
+    }
+    float *part = sm + kAttnTailMaxKv; // NW rows of hd partial sums
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        acc[e] = group_sum(acc[e], seg);
+    if (lane % seg == 0)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            part[wave * hd + vl * 8 + e] = acc[e];
+    __syncthreads();
+    if (2 * tid < hd)
+    {
+        float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+        for (uint32_t w = 0; w < NW; ++w)
+        {
+            o0 += part[w * hd + 2 * tid];
+            o1 += part[w * hd + 2 * tid + 1];
+        }
+        store_pair<false>(out + 2 * tid, o0, o1);
+    }
+    __syncthreads();
+}
+
+// EPI_QKV_ATTN after the workgroup's last unit: each head's completed units are counted (the wave's stores are
+// agent-scope and complete first, the same hand-off as the vocabulary product's arg max), and the workgroup whose
+// count completes a head computes that head's attention. No workgroup waits for another.
+template <int R>
+__device__ __forceinline__ void qkv_attention_heads(const GemvArgs &a, uint32_t *head_done, float *sm)
+{
+    __shared__ uint32_t todo[kAttnTailMaxHeads];
+    __shared__ uint32_t ntodo;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t per_head = 3 * a.hd / R; // units holding a head's q, k and v rows
+    __builtin_amdgcn_s_waitcnt(0);
+    if (tid == 0)
+        ntodo = 0;
+    __syncthreads();
+    if (tid < a.H && head_done[tid] != 0)
+    {
+        const uint32_t n = head_done[tid];
+        if (__hip_atomic_fetch_add(a.head_count + tid, n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + n == per_head)
+            todo[atomicAdd(&ntodo, 1u)] = tid;
+    }
+    __syncthreads();
+    const uint32_t n = ntodo;
+    if (n == 0)
+        return;
+    if (a.step->offset + 1 > kAttnTailMaxKv)
+    {
+        // a position past what the launch was chosen for (the host picks the kernel by position): flag the step
+        if (tid == 0 && a.attn_err)
+            __hip_atomic_store(a.attn_err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        for (uint32_t i = 0; i < n && tid == 0; ++i)
+            __hip_atomic_store(a.head_count + todo[i], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
+    // the completing workgroup acquires what the head's other workgroups stored
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    for (uint32_t i = 0; i < n; ++i)
+    {
+        const uint32_t head = todo[i];
+        qkv_attention_tail(a, head, sm);
+        if (tid == 0)
+            __hip_atomic_store(a.head_count + head, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 template <int EPI, int R, int NV> __global__ __launch_bounds__(256) void gemv_fast_kernel(GemvArgs a, uint32_t units)
 {
     extern __shared__ u32x4 xs[];
@@ -434,6 +607,12 @@ template <int EPI, int R, int NV> __global__ __launch_bounds__(256) void gemv_fa
     const uint32_t nvec = a.K / 8;
     // the residual products (Wo, Wd) take their input as is; the others normalise it (the launcher checks norm_w)
     constexpr bool norm = gemv_normalises(EPI);
+
+    // EPI_QKV_ATTN: units completed per head by this workgroup
+    __shared__ uint32_t head_done[EPI == EPI_QKV_ATTN ? kAttnTailMaxHeads : 1];
+    if constexpr (EPI == EPI_QKV_ATTN)
+        if (tid < kAttnTailMaxHeads)
+            head_done[tid] = 0;
 
     // 1. input share (and RMSNorm weights)
     // Loads are unconditional at clamped addresses (a guarded load compiles to a branch and a full wait per load);
@@ -464,7 +643,7 @@ template <int EPI, int R, int NV> __global__ __launch_bounds__(256) void gemv_fa
     uint32_t rows[R];
     // the epilogue's inputs (RoPE denominators, residuals), requested ahead of the unit's weights: a request in the
     // epilogue would wait for the next unit's weights, as counters retire in issue order
-    constexpr int NF = EPI == EPI_QKV && R >= 2 ? R / 2 : 1, NR = EPI == EPI_RESID ? R : 1;
+    constexpr int NF = is_qkv(EPI) && R >= 2 ? R / 2 : 1, NR = EPI == EPI_RESID ? R : 1;
     float fq[NF], rs[NR];
 #pragma unroll
     for (int k = 0; k < NF; ++k)
@@ -474,7 +653,7 @@ template <int EPI, int R, int NV> __global__ __launch_bounds__(256) void gemv_fa
         rs[k] = 0.f;
     auto load_unit = [&](uint32_t unit) {
         gemv_rows_of<EPI>(a, unit, R, rows);
-        if (EPI == EPI_QKV)
+        if (is_qkv(EPI))
 #pragma unroll
             for (int k = 0; k < NF; ++k)
                 fq[k] = a.freqs[((unit < units && rows[2 * k] < a.rows ? rows[2 * k] : 0) % a.D) % a.hd / 2];
@@ -574,6 +753,8 @@ template <int EPI, int R, int NV> __global__ __launch_bounds__(256) void gemv_fa
         if (lane == 0)
         {
             gemv_epilogue<EPI, R>(a, cur, cur_rows, acc, cur_fq, cur_rs);
+            if constexpr (EPI == EPI_QKV_ATTN)
+                atomicAdd(&head_done[(cur_rows[0] % a.D) / a.hd], 1u);
             if constexpr (EPI == EPI_ARGMAX)
 #pragma unroll
                 for (int k = 0; k < R; ++k)
@@ -589,6 +770,8 @@ template <int EPI, int R, int NV> __global__ __launch_bounds__(256) void gemv_fa
     }
     if constexpr (EPI == EPI_ARGMAX)
         gemv_argmax_finish(a, bv, bi);
+    if constexpr (EPI == EPI_QKV_ATTN)
+        qkv_attention_heads<R>(a, head_done, (float *)xs);
 }
 
 // units of R rows for `a`; 0 when R does not fit the epilogue's pairing
@@ -596,7 +779,7 @@ static uint32_t gemv_units(int epi, const GemvArgs &a, int R)
 {
     if (epi == EPI_GATEUP)
         return (R % 2 == 0 && a.rows % R == 0) ? a.rows / R : 0;
-    if (epi == EPI_QKV && R % 2 != 0)
+    if (is_qkv(epi) && R % 2 != 0)
         return 0;
     return (a.rows + R - 1) / R;
 }
@@ -608,7 +791,9 @@ template <int EPI, int R, int NV> static hipError_t launch_fast(hipStream_t st, 
         return hipErrorInvalidValue;
     // resident workgroups per CU at this kernel's register use and this K's LDS (at least 1: it only sizes the grid)
     static uint64_t occ_memo = 0;
-    const size_t lds = (size_t)a.K * 2;
+    // the input row (EPI_QKV_ATTN: at least the attention tail's scores and partial sums)
+    const size_t lds = EPI == EPI_QKV_ATTN ? std::max((size_t)a.K * 2, (kAttnTailMaxKv + 4 * a.hd) * sizeof(float))
+                                           : (size_t)a.K * 2;
     const int per_cu = std::max(occupancy_per_cu((const void *)gemv_fast_kernel<EPI, R, NV>, 256, lds, occ_memo), 1);
     // every wave gets the same number of units (the fewest that the resident waves can cover), so no wave runs an
     // extra unit while the others idle. Kernels of at most 4 resident workgroups per CU (two rows per unit, or long
@@ -695,7 +880,7 @@ static hipError_t launch_argmax_epi(hipStream_t st, const GemvArgs &a, int cu_co
 static int gemv_default_r(int epi, uint32_t K)
 {
     (void)K;
-    return epi == EPI_GATEUP || epi == EPI_QKV ? 2 : 1;
+    return epi == EPI_GATEUP || is_qkv(epi) ? 2 : 1;
 }
 
 hipError_t launch_gemv(hipStream_t st, int epi, const GemvArgs &a, int cu_count)
@@ -704,8 +889,12 @@ hipError_t launch_gemv(hipStream_t st, int epi, const GemvArgs &a, int cu_count)
         return hipErrorInvalidValue;
     const uint32_t nvec = a.K / 8;
     int R = a.rows_per_unit ? (int)a.rows_per_unit : gemv_default_r(epi, a.K);
-    if (R == 1 && (epi == EPI_GATEUP || epi == EPI_QKV))
+    if (R == 1 && (epi == EPI_GATEUP || is_qkv(epi)))
         R = 2;
+    // the attention tail: a head's V row as 4 to 64 16-byte vectors (a lane each)
+    if (epi == EPI_QKV_ATTN && (R != 2 || a.H > kAttnTailMaxHeads || a.hd % 8 != 0 || a.hd < 32 ||
+                                64 % (a.hd / 8) != 0 || !a.head_count || !a.attn_out))
+        return hipErrorInvalidValue;
     const int NV = (R == 1 || R == 2 || R == 4) ? gemv_pick_nv(R, nvec) : 0;
     if (NV != 0 && (epi != EPI_GATEUP || a.rows % R == 0))
     {
@@ -721,13 +910,15 @@ hipError_t launch_gemv(hipStream_t st, int epi, const GemvArgs &a, int cu_count)
             return launch_epi<EPI_GATEUP>(st, a, cu_count, R, NV);
         case EPI_QKV:
             return launch_epi<EPI_QKV>(st, a, cu_count, R, NV);
+        case EPI_QKV_ATTN:
+            return launch_epi<EPI_QKV_ATTN>(st, a, cu_count, R, NV);
         case EPI_ARGMAX:
             return R == 1 ? launch_argmax_epi(st, a, cu_count, NV) : hipErrorInvalidValue;
         default:
             return hipErrorInvalidValue;
         }
     }
-    return epi == EPI_ARGMAX ? hipErrorInvalidValue : launch_gemv_loop(st, epi, a, cu_count);
+    return epi == EPI_ARGMAX || epi == EPI_QKV_ATTN ? hipErrorInvalidValue : launch_gemv_loop(st, epi, a, cu_count);
 }
 
 // ---------------------------------------------------------------------------------------------------------------

@@ -80,7 +80,14 @@ enum GemvEpi : int
     // clears the counter (no workgroup waits for another)
     EPI_ARGMAX = 4,
     EPI_RAW = 5, // EPI_PLAIN's out from the input as given, no RMSNorm (the MATMUL op's mat_mul_vec case)
+    // EPI_QKV, then each head's single-token attention (kv = step->offset + 1 <= kAttnTailMaxKv) computed by the
+    // workgroup that completes the head's q, k and v rows: attn_out[h*hd + d] as the short-cache attention kernel
+    // leaves it. head_count [H] counts completed units per head (zero between launches).
+    EPI_QKV_ATTN = 6,
 };
+// the decode QKV product's attention tail: heads at most, and positions at most (its scores and partial sums reuse
+// the GEMV's input LDS, sized to hold kAttnTailMaxKv + 4 * hd floats)
+constexpr uint32_t kAttnTailMaxHeads = 64, kAttnTailMaxKv = 512;
 
 struct GemvArgs
 {
@@ -99,6 +106,12 @@ struct GemvArgs
     const Step *step;
     const float *freqs;     // base^(2w/hd), w < hd/2
     uint32_t D, hd, ctx;
+    // EPI_QKV_ATTN
+    uint16_t *attn_out;     // [H, hd]
+    uint32_t *head_count;   // [H]
+    uint32_t H;
+    float attn_scale;
+    uint32_t *attn_err;     // set (system scope) when the step's position exceeds kAttnTailMaxKv
     // EPI_ARGMAX (fast kernel only, one row per unit; a launch of more than am_cap workgroups is refused)
     uint32_t *am_ids;   // [1]
     DecodeIo *am_io;    // optional
