@@ -68,16 +68,18 @@ def _vk_shape(shape):
                 vocab=shape["vocab"], ctx=shape["ctx"])
 
 
-@pytest.mark.parametrize("path", ["long", "attn_o"])
+@pytest.mark.parametrize("path", ["long", "attn_o", "persist"])
 def test_decode_recovers_when_a_wait_gives_up(ctx, vk, oracle, monkeypatch, capfd, path):
     """VKLLM_SPIN_LIMIT=0 makes every bounded wait give up at once, without polling, so each kernel still exits
-    normally: the one-kernel long-cache attention (1100-token prompt, chunks of 256 positions) or the attention +
-    Wo launch (VKLLM_ATTN_O=1, a short cache). The step must notice, clear the counters, switch to the attention
-    kernels that never wait and run again: ids equal to the oracle's, logits within 2e-2, and every later step on
-    the waiting-free path."""
+    normally: the one-kernel long-cache attention (1100-token prompt, chunks of 256 positions), the attention +
+    Wo launch (VKLLM_ATTN_O=1, a short cache) or the persistent step's grid barriers (VKLLM_PERSIST=1, a short
+    cache). The step must notice, clear the counters, switch to the kernels that never wait and run again: ids equal
+    to the oracle's, logits within 2e-2, and every later step on the waiting-free path."""
     monkeypatch.setenv("VKLLM_SPIN_LIMIT", "0")
-    if path == "attn_o":
-        monkeypatch.setenv("VKLLM_ATTN_O", "1")
+    if path in ("attn_o", "persist"):
+        monkeypatch.setenv("VKLLM_PERSIST", "1" if path == "persist" else "0")
+        if path == "attn_o":
+            monkeypatch.setenv("VKLLM_ATTN_O", "1")
         shape = dict(n_layer=2, dim=4096, n_head=32, ffn=11008, vocab=32000, ctx=96)
         prompt_len = 20
     else:

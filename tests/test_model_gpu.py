@@ -212,6 +212,7 @@ def test_long_context_decode(ctx, vk, oracle, monkeypatch, small_max, long_one):
     8 chunks of 256 positions per head, merged by the last chunk's block, in one launch or in two."""
     monkeypatch.setenv("VKLLM_ATTN_SMALL_MAX", small_max)
     monkeypatch.setenv("VKLLM_ATTN_LONG", long_one)
+    monkeypatch.setenv("VKLLM_PERSIST", "0")  # the separate attention kernels (the persistent step has its own tests)
     shape = dict(n_layer=2, dim=256, n_head=2, ffn=512, vocab=1000, ctx=2048)
     ids, want_ids, err = _gpu_vs_oracle(ctx, vk, oracle, shape, seed=5, prompt_len=1000, n_steps=8, prompt_seed=6)
     assert err.max() <= LOGIT_TOL
@@ -233,6 +234,7 @@ def test_attention_and_projection_in_one_launch(ctx, vk, monkeypatch):
     the attention workgroups) against the two separate launches, at the 7B widths: identical ids and logits."""
     shape = dict(n_layer=2, dim=4096, n_head=32, ffn=11008, vocab=32000, ctx=160)
     prompt = vk.prompt_tokens(8, 20, shape["vocab"])
+    monkeypatch.setenv("VKLLM_PERSIST", "0")
     monkeypatch.setenv("VKLLM_ATTN_O", "1")
     ids_a, logits_a = _device_loop(ctx, vk, shape, 7, prompt, 24)
     monkeypatch.setenv("VKLLM_ATTN_O", "0")
@@ -256,6 +258,8 @@ def test_arg_max_in_the_vocabulary_product(ctx, vk, monkeypatch):
     w = np.zeros((shape["vocab"], shape["dim"]), np.float16)
     w[plus] = 0.01
     w[minus] = -0.01
+
+    monkeypatch.setenv("VKLLM_PERSIST", "0")
 
     def run(epi):
         monkeypatch.setenv("VKLLM_ARGMAX_EPI", epi)

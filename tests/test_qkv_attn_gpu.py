@@ -52,6 +52,7 @@ def test_decode_attention_in_qkv_launch(ctx, vk, oracle, monkeypatch, name, tail
     shape = SHAPES[name]
     hd = shape["dim"] // shape["n_head"]
     monkeypatch.setenv("VKLLM_QKV_ATTN", tail)  # read when the model's first step sets up its state
+    monkeypatch.setenv("VKLLM_PERSIST", "0")  # the separate decode kernels
     cfg = oracle.make_cfg(**shape)
     ref = oracle.Model(cfg=cfg, seed=91)
     vcfg = vk.llama_config(shape["n_layer"], shape["dim"], shape["n_head"], shape["ffn"], shape["vocab"],

@@ -107,6 +107,17 @@ struct FusedState
     // counts, zero between launches.
     bool qkv_attn = false, qkv_attn_now = false;
     uint32_t *head_count = nullptr;
+    // single-token steps with short caches as one persistent launch after the embedding (VKLLM_PERSIST=1; the
+    // default is the separate kernels, which measure faster at the 7B shape); cleared when a wait of that launch
+    // gives up or the device cannot hold its grid. Its activations: the residual stream [2L + 1] rows, q, attention
+    // output [L] rows, FFN activations [L] rows (each row written once per step), the layers' weight pointers, and
+    // the barrier words (zero between launches).
+    bool persist = false;
+    vk::PersistLayer *persist_layers = nullptr;
+    uint16_t *p_hs = nullptr, *p_qs = nullptr, *p_attns = nullptr, *p_acts = nullptr;
+    uint32_t p_hstride = 0, p_fstride = 0;
+    uint32_t *persist_sync = nullptr;
+    bool p_variant[kSmallBuckets + 1] = {}; // per attention variant: its steps are enqueued as the persistent launch
     // long caches in one attention kernel (VKLLM_ATTN_LONG=0: two); cleared when the device cannot hold every chunk
     // block at once
     bool attn_long = true;
@@ -282,7 +293,9 @@ void fused_model_release(vkllm_context *ctx, vkllm_models_llama2 *model)
         (void)hipFree(fs->freqs);
     free_stream_tiles(fs);
     void *att[] = {fs->att_scores, fs->att_stats, fs->att_part, fs->att_count, fs->attn_sync, fs->att_long_sync,
-                   fs->gemm_work,  fs->am_val,    fs->am_idx,   fs->am_count,  fs->head_count};
+                   fs->gemm_work,  fs->am_val,    fs->am_idx,   fs->am_count,  fs->head_count,
+                   fs->persist_layers, fs->p_hs,     fs->p_qs,     fs->p_attns,   fs->p_acts,
+                   fs->persist_sync};
     for (void *b : att)
         if (b)
             (void)hipFree(b);
@@ -415,6 +428,27 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
                        mp->hd >= 32 && 64 % (mp->hd / 8) == 0;
         HIP_TRY(hipMalloc(&fs->head_count, (size_t)mp->H * sizeof(uint32_t)));
         HIP_TRY(hipMemset(fs->head_count, 0, (size_t)mp->H * sizeof(uint32_t)));
+        const char *pe = getenv("VKLLM_PERSIST");
+        fs->persist = pe && *pe == '1';
+        {
+            std::vector<vk::PersistLayer> pl(mp->L);
+            for (uint32_t l = 0; l < mp->L; ++l)
+            {
+                const ModelPriv::Layer &ly = mp->layers[l];
+                pl[l] = {ly.wqkv, ly.wo, ly.wug, ly.wd, ly.attn_norm, ly.ffn_norm, ly.kc, ly.vc};
+            }
+            HIP_TRY(hipMalloc(&fs->persist_layers, pl.size() * sizeof(vk::PersistLayer)));
+            HIP_TRY(hipMemcpy(fs->persist_layers, pl.data(), pl.size() * sizeof(vk::PersistLayer),
+                              hipMemcpyHostToDevice));
+            fs->p_hstride = (mp->D + 127) / 128 * 128;
+            fs->p_fstride = (mp->F + 127) / 128 * 128;
+            HIP_TRY(hipMalloc(&fs->p_hs, (size_t)(2 * mp->L + 1) * fs->p_hstride * 2));
+            HIP_TRY(hipMalloc(&fs->p_qs, (size_t)mp->L * fs->p_hstride * 2));
+            HIP_TRY(hipMalloc(&fs->p_attns, (size_t)mp->L * fs->p_hstride * 2));
+            HIP_TRY(hipMalloc(&fs->p_acts, (size_t)mp->L * fs->p_fstride * 2));
+            HIP_TRY(hipMalloc(&fs->persist_sync, vk::kPersistSyncWords * sizeof(uint32_t)));
+            HIP_TRY(hipMemset(fs->persist_sync, 0, vk::kPersistSyncWords * sizeof(uint32_t)));
+        }
         const char *al = getenv("VKLLM_ATTN_LONG");
         fs->attn_long = !(al && *al == '0');
         const char *re = getenv("VKLLM_ROPE_EPI");
@@ -661,6 +695,45 @@ static uint32_t decode_variant(const FusedState *fs, uint32_t kv)
     return kv <= fs->attn_small_max ? (kv - 1) / kSmallBucket : kSmallBuckets;
 }
 
+// The persistent step after the embedding (its input row, fs->p_hs[0]) for the current slot and short-cache bound
+static hipError_t launch_persist(vkllm_context *ctx, ModelPriv *mp)
+{
+    FusedState *fs = mp->fs;
+    vk::PersistArgs pa{};
+    pa.layers = fs->persist_layers;
+    pa.L = mp->L;
+    pa.D = mp->D;
+    pa.F = mp->F;
+    pa.V = mp->V;
+    pa.H = mp->H;
+    pa.hd = mp->hd;
+    pa.ctx = mp->ctx;
+    pa.eps = mp->eps;
+    pa.scale = 1.0f / sqrtf((float)mp->hd);
+    pa.step = fs->step;
+    pa.freqs = fs->freqs;
+    pa.out_norm = mp->out_norm;
+    pa.out_w = mp->out_w;
+    pa.hs = fs->p_hs;
+    pa.qs = fs->p_qs;
+    pa.attns = fs->p_attns;
+    pa.acts = fs->p_acts;
+    pa.hstride = fs->p_hstride;
+    pa.fstride = fs->p_fstride;
+    pa.logits = fs->slot_logits + (size_t)fs->slot * mp->V;
+    pa.small_max = fs->small_kv_max;
+    pa.sync = fs->persist_sync;
+    pa.err = &fs->dio->err;
+    pa.spin_limit = fs->attn_o_spin_limit;
+    pa.am_ids = fs->slot_ids + fs->slot;
+    pa.am_io = fs->dio;
+    pa.am_val = fs->am_val;
+    pa.am_idx = fs->am_idx;
+    pa.am_count = fs->am_count;
+    pa.am_cap = kArgmaxCandidates;
+    return vk::launch_decode_persist(ctx->device->stream, pa, ctx->device->cu_count);
+}
+
 // decode: S == 1, position from fs->step; `variant` (decode_variant) picks the attention kernels and, for short caches,
 // the positions bound of their launches
 static vkllm_err_t enqueue_decode(vkllm_context *ctx, ModelPriv *mp, uint32_t variant)
@@ -670,6 +743,22 @@ static vkllm_err_t enqueue_decode(vkllm_context *ctx, ModelPriv *mp, uint32_t va
     {
         const uint32_t end = (variant + 1) * kSmallBucket;
         mp->fs->small_kv_max = end < mp->fs->attn_small_max ? end : mp->fs->attn_small_max;
+    }
+    if (small_attn && mp->fs->persist && !ctx->device->timing)
+    {
+        // the embedding row, then every layer and the vocabulary product in one launch
+        FusedState *fs = mp->fs;
+        KTRY(ctx, KID_F_EMBED,
+             vk::launch_embed_decode(ctx->device->stream, fs->dio, fs->step, mp->embd, fs->p_hs, mp->V, mp->D,
+                                     mp->pad_id, fs->slot_ids + (1 - fs->slot)));
+        const hipError_t e = launch_persist(ctx, mp);
+        fs->p_variant[variant] = e == hipSuccess;
+        if (e == hipSuccess)
+            return VKLLM_ERR_OK;
+        if (e == hipErrorInvalidConfiguration) // the device does not hold the grid: separate kernels from now on
+            fs->persist = false;
+        else if (e != hipErrorInvalidValue) // (a shape or positions bound the launch does not take: this bucket)
+            return hip_fail(e, "launch_decode_persist", __FILE__, __LINE__);
     }
     // caches of at most kAttnTailMaxKv positions (this bucket's end): the attention in the QKV product's launch
     const bool tail_attn = small_attn && mp->fs->qkv_attn && mp->fs->small_kv_max <= vk::kAttnTailMaxKv;
@@ -1037,9 +1126,11 @@ vkllm_err_t fused_plan_run(vkllm_context *ctx, vkllm_graph *graph)
             HIP_TRY(hipMemsetAsync(fs->attn_sync, 0, vk::kAttnSyncWords * sizeof(uint32_t), st));
             HIP_TRY(hipMemsetAsync(fs->att_long_sync, 0, (size_t)mp->H * vk::kAttnLongStride * sizeof(uint32_t), st));
             HIP_TRY(hipMemsetAsync(fs->att_count, 0, (size_t)mp->H * sizeof(uint32_t), st));
+            HIP_TRY(hipMemsetAsync(fs->persist_sync, 0, vk::kPersistSyncWords * sizeof(uint32_t), st));
             drop_graphs(fs);
             fs->attn_long = false;
             fs->attn_o = false;
+            fs->persist = false;
             fs->dio->offset = p->offset;
             fs->dio->token = toks[0];
             fs->dio->token_dev = 0;
@@ -1136,12 +1227,12 @@ extern "C" vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *ctx, st
     // the launches below recompute the last completed step (same token, same position): a step launched ahead is
     // dropped first, so that nothing is mistaken for it
     _CHECK(discard_ahead(ctx, fs));
-    const bool whole = strcmp(family, "decode_step") == 0;
+    const bool whole = strcmp(family, "decode_step") == 0, persist = strcmp(family, "decode_persist") == 0;
     int kid = -1;
     for (const auto &f : families)
         if (strcmp(family, f.name) == 0)
             kid = f.kid;
-    _CHECK_ARGS(whole || kid >= 0);
+    _CHECK_ARGS(whole || persist || kid >= 0);
     const int replay = (int)decode_variant(fs, fs->done_offset + 1);
     if (whole && (fs->last_exec < 0 || !fs->exec[fs->done_slot][replay]))
     {
@@ -1163,14 +1254,24 @@ extern "C" vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *ctx, st
             fs->small_kv_max = end < fs->attn_small_max ? end : fs->attn_small_max;
         }
         fs->qkv_attn_now = b < kSmallBuckets && fs->qkv_attn && fs->small_kv_max <= vk::kAttnTailMaxKv;
+        if (persist && (b >= kSmallBuckets || !fs->persist || !fs->p_variant[b]))
+        {
+            log_error("decode_persist timing needs a last single-token step that ran as the persistent launch");
+            return VKLLM_ERR_ARGS;
+        }
     }
     hipStream_t st = ctx->device->stream;
     // the residual GEMVs write into fs->xn (a scratch row) so that repeating them leaves the model state unchanged
     auto launch = [&](uint32_t r) -> hipError_t {
         if (whole)
             return hipGraphLaunch(fs->exec[fs->done_slot][replay], st);
+        if (persist) // the last step again from its embedding row (same token and position: same cache rows)
+            return launch_persist(ctx, mp);
         return launch_decode_kernel(ctx, mp, (KernelId)kid, r % mp->L, fs->xn);
     };
+    if (persist) // the last step's embedding row and position again (a step launched ahead wrote its own)
+        HIP_TRY(vk::launch_embed_decode(st, fs->dio, fs->step, mp->embd, fs->p_hs, mp->V, mp->D, mp->pad_id,
+                                        fs->slot_ids + (1 - fs->slot)));
     // one untimed launch so the first timed one does not pay for code loading
     HIP_TRY(launch(0));
     hipEvent_t ev[2];

@@ -384,137 +384,6 @@ __global__ __launch_bounds__(256) void attn_long_kernel(AttnDecodeArgs a)
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// short caches: one block of 512 threads per (head, dim slice). The work is latency-bound: the block has its first
-// keys and V rows in flight before it knows the position, each wave reduces the softmax statistics on its own, and
-// the P.V partials are reduced inside each wave before one exchange through LDS. LDS holds kv floats of scores.
-// the reference's transposed product (kv == hd): out[r] = fp16(sum_k p_k V[r][k]) for this block's rows, two per
-// thread
-template <bool AGENT>
-__device__ __forceinline__ void pv_transposed_pairs(const float *pl, const uint16_t *Vh, uint16_t *out, uint32_t kv,
-                                                    uint32_t hd, uint32_t d0, uint32_t dg)
-{
-    for (uint32_t r = 2 * threadIdx.x; r < dg; r += 2 * blockDim.x)
-    {
-        const uint16_t *row0 = Vh + (size_t)(d0 + r) * hd, *row1 = row0 + hd;
-        float a0 = 0.f, a1 = 0.f;
-        for (uint32_t k = 0; k < kv; ++k)
-        {
-            a0 = fmaf(pl[k], h2f(row0[k]), a0);
-            a1 = fmaf(pl[k], h2f(row1[k]), a1);
-        }
-        store_pair<AGENT>(out + r, a0, a1);
-    }
-}
-
-// Block (h, g) of the short-cache attention: all kv keys of head h scored, the softmax statistics, then the
-// probability-weighted sum of dims [g dg, (g + 1) dg) of V.
-// The first two batches of keys and two passes of V rows (512 positions at head_dim 128) are requested before the
-// position is known, at rows clamped to the launch's largest cache length small_max (further V passes follow the
-// keys): a launch for short caches asks HBM for no row past small_max, the clamped requests repeat a row already in
-// flight. Rows at or past kv never reach a score or a sum (their scores are not stored and their V values are
-// replaced by zeros, whatever the cache holds there). After the scores are in LDS every wave reduces the statistics
-// itself, so no further exchange is needed until the P.V partials.
-template <int NT, bool AGENT>
-__device__ __forceinline__ void small_block(const AttnDecodeArgs &a, uint32_t h, uint32_t g, float *sm, float *red)
-{
-    constexpr uint32_t NW = NT / 64;
-    constexpr int U = 4, UV = kSmallMaxPasses;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t dg = a.hd / a.groups, d0 = g * dg, vpr = a.hd / 8, last = min(a.small_max, a.ctx) - 1;
-    // V layout: lane = (vector vl of the slice, row slot); a wave covers seg rows, the block rpp rows per pass
-    const uint32_t lpr = dg / 8, seg = 64 / lpr;
-    const uint32_t vl = lane / seg, vs = wave * seg + lane % seg, rpp = NW * seg;
-    const uint16_t *Vh = a.vc + (size_t)h * a.ctx * a.hd;
-    const u32x4 *Vv = (const u32x4 *)Vh + d0 / 8 + vl;
-    u32x4 vv[UV];
-    vv[0] = Vv[(size_t)min(vs, last) * vpr];
-    vv[1] = Vv[(size_t)min(vs + rpp, last) * vpr];
-    const KeyLayout k = key_layout<NT>(a.q + (size_t)h * a.hd, a.hd);
-    const u32x4 *Kv = (const u32x4 *)(a.kc + (size_t)h * a.ctx * a.hd);
-    const uint32_t step = k.kpp * U;
-    u32x4 ka[U], kb[U], na[U], nb[U];
-    load_keys<U>(k, Kv, k.ks, last, ka, kb);
-    load_keys<U>(k, Kv, k.ks + step, last, na, nb);
-    const uint32_t kv = a.step->offset + 1;
-    const uint32_t passes = (kv + rpp - 1) / rpp;
-    const uint32_t nit = (kv + step - 1) / step;
-    for (uint32_t it = 0; it < nit; ++it)
-    {
-        score_keys<U>(k, ka, kb, k.ks + it * step, kv, a.scale, sm);
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-        {
-            ka[u] = na[u];
-            kb[u] = nb[u];
-        }
-        if (it + 2 < nit)
-            load_keys<U>(k, Kv, k.ks + (it + 2) * step, kv - 1, na, nb);
-    }
-    // V rows past the first two passes (kv > 2 rpp) once the key registers are free
-#pragma unroll
-    for (int t = 2; t < UV; ++t)
-        if ((uint32_t)t < passes)
-            vv[t] = Vv[(size_t)min(vs + rpp * t, kv - 1) * vpr];
-    __syncthreads();
-    // softmax statistics, reduced by every wave over all kv scores (same values, same order in each wave)
-    float M = -FLT_MAX;
-    for (uint32_t j = lane; j < kv; j += 64)
-        M = fmaxf(M, sm[j]);
-    M = wave_max_dpp(M);
-    float L = 0.f;
-    for (uint32_t j = lane; j < kv; j += 64)
-        L += expf(sm[j] - M);
-    L = wave_sum_dpp(L);
-    uint16_t *out = a.out + (size_t)h * a.hd + d0;
-    if (kv == a.hd)
-    {
-        __syncthreads(); // every wave has its statistics before the scores become probabilities
-        for (uint32_t j = tid; j < kv; j += NT)
-            sm[j] = h2f(f2h(expf(sm[j] - M) / L));
-        __syncthreads();
-        pv_transposed_pairs<AGENT>(sm, Vh, out, kv, a.hd, d0, dg);
-        return;
-    }
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int t = 0; t < UV; ++t)
-    {
-        const uint32_t j = vs + rpp * t;
-        if ((uint32_t)t < passes) // block-uniform
-        {
-            const bool live = j < kv;
-            const float pj = live ? h2f(f2h(expf(sm[min(j, kv - 1)] - M) / L)) : 0.f;
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-            {
-                const uint32_t v = live ? vv[t][e] : 0u;
-                acc[2 * e] = fmaf(pj, half_lo(v), acc[2 * e]);
-                acc[2 * e + 1] = fmaf(pj, half_hi(v), acc[2 * e + 1]);
-            }
-        }
-    }
-    float *part = red; // NW rows of dg partial sums
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-        acc[e] = seg_sum(acc[e], seg);
-    if (lane % seg == seg - 1)
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-            part[wave * dg + vl * 8 + e] = acc[e];
-    __syncthreads();
-    if (2 * tid < dg)
-    {
-        float o0 = 0.f, o1 = 0.f;
-#pragma unroll
-        for (uint32_t w = 0; w < NW; ++w)
-        {
-            o0 += part[w * dg + 2 * tid];
-            o1 += part[w * dg + 2 * tid + 1];
-        }
-        store_pair<AGENT>(out + 2 * tid, o0, o1);
-    }
-}
-
 // block b of the short-cache attention (blocks of heads >= H do nothing). A position past the launch's small_max
 // (the LDS's positions and the speculative loads' bound) is a host error: the block raises the step's error flag
 // and writes nothing.

@@ -181,6 +181,44 @@ struct AttnOArgs
 };
 hipError_t launch_attn_o(hipStream_t st, const AttnOArgs &a, uint32_t kv_max, int cu_count);
 
+// ---- persistent single-token step (decode_persist.hip): every layer and the vocabulary product in one launch ----
+struct PersistLayer
+{
+    const uint16_t *wqkv, *wo, *wug, *wd; // [3D, D], [D, D], [2F, D] (up rows, then gate rows), [D, F]
+    const float *attn_norm, *ffn_norm;
+    uint16_t *kc, *vc; // [H, ctx, hd]
+};
+struct PersistArgs
+{
+    const PersistLayer *layers; // [L], device memory
+    uint32_t L, D, F, V, H, hd, ctx;
+    float eps, scale;
+    const Step *step; // the step's position (written by the embedding kernel)
+    const float *freqs;
+    const float *out_norm;
+    const uint16_t *out_w;
+    // activations, each row written once per step and read only after it is written: hs [2L + 1][hstride] the
+    // residual stream (hs[0] the embedding row, hs[2l + 1] after layer l's attention, hs[2l + 2] after its FFN),
+    // qs and attns [L][hstride], acts [L][fstride]; strides in halves, multiples of 128
+    uint16_t *hs, *qs, *attns, *acts;
+    uint32_t hstride, fstride;
+    uint16_t *logits;   // [V]
+    uint32_t small_max; // the attention's positions bound (its LDS and speculative cache reads)
+    uint32_t *sync;     // kPersistSyncWords, zero before the first launch; every launch leaves them zero
+    uint32_t *err;      // set (system scope) when a wait gives up; the step's outputs are then not valid
+    uint32_t spin_limit;
+    // the arg max (as GemvArgs' EPI_ARGMAX fields)
+    uint32_t *am_ids;
+    DecodeIo *am_io;
+    float *am_val;
+    uint32_t *am_idx, *am_count;
+    uint32_t am_cap;
+};
+constexpr uint32_t kPersistSyncWords = 12 * 64;
+// hipErrorInvalidValue: a shape without a compiled instantiation, or a positions bound the attention part does not
+// take (nothing launched); hipErrorInvalidConfiguration: fewer than one resident workgroup per CU at this LDS size
+hipError_t launch_decode_persist(hipStream_t st, const PersistArgs &a, int cu_count);
+
 // prefill: queries s < S at positions offset+s attend to positions <= offset+s (the row max over all offset+S);
 // head sizes 64 and 128 run on the MFMA kernel, others one workgroup per (row, head)
 bool attn_prefill_mfma_ok(uint32_t hd);
