@@ -691,6 +691,105 @@ template <int EPI, int R, int NV> __global__ __launch_bounds__(256) void gemv_fa
         qkv_attention_heads<R>(a, head_done, (float *)xs);
 }
 
+// Residual GEMV over long rows (K > 8192: the down product, K = FFN width): a workgroup per unit of R rows, its 4
+// waves splitting each row's 16-byte vectors (wave w, lane l: vectors 64 w + l + 256 i, i < NVW). A wave streaming a
+// whole 22 KB row by itself reads at 5.4 TB/s on this GPU; spread over the workgroup the same bytes stream at
+// 6.8-6.9 TB/s. The workgroup takes units blockIdx.x + n gridDim.x (n < kWgMaxUnits); each wave reduces its partial
+// sums per unit into LDS without waiting for the others (the next unit's weights are requested before the
+// reduction), and after the last unit thread t finishes row t: out[r] = fp16(resid[r] + fp16(sum)), the four wave
+// partials added in wave order, the residual requested when the kernel starts.
+constexpr uint32_t kWgMaxUnits = 8;
+template <int R, int NVW> __global__ __launch_bounds__(256) void gemv_wg_resid_kernel(GemvArgs a, uint32_t units)
+{
+    extern __shared__ u32x4 xs[];
+    __shared__ float part[kWgMaxUnits][4][R];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+    const uint32_t nvec = a.K / 8;
+    // 1. the input row (loads unconditional at clamped addresses; lanes past the end are zeroed below), and the
+    // residual of the row this thread finishes
+    u32x4 xr[NVW];
+#pragma unroll
+    for (int i = 0; i < NVW; ++i)
+        xr[i] = ((const u32x4 *)a.x)[min(tid + 256 * i, nvec - 1)];
+    const uint32_t my_unit = blockIdx.x + (tid / R) * gridDim.x, my_row = my_unit * R + tid % R;
+    const bool finisher = tid < kWgMaxUnits * R && my_unit < units && my_row < a.rows;
+    const float my_rs = h2f(a.resid[finisher ? my_row : 0]);
+    // 2. the first unit's weights
+    u32x4 w[R][NVW];
+    auto load_unit = [&](uint32_t unit) {
+#pragma unroll
+        for (int k = 0; k < R; ++k)
+        {
+            const u32x4 *wr = (const u32x4 *)(a.w + (size_t)min(unit * R + k, a.rows - 1) * a.K);
+#pragma unroll
+            for (int i = 0; i < NVW; ++i)
+                w[k][i] = __builtin_nontemporal_load(wr + min(tid + 256 * i, nvec - 1));
+        }
+    };
+    uint32_t u = blockIdx.x;
+    if (u < units)
+        load_unit(u);
+#pragma unroll
+    for (int i = 0; i < NVW; ++i)
+    {
+        const uint32_t vi = tid + 256 * i;
+        if (vi < nvec)
+            xs[vi] = xr[i];
+    }
+    __syncthreads();
+    // 3. units
+    for (uint32_t n = 0; u < units; u += gridDim.x, ++n)
+    {
+        float acc[R];
+#pragma unroll
+        for (int k = 0; k < R; ++k)
+            acc[k] = 0.f;
+#pragma unroll
+        for (int i = 0; i < NVW; ++i)
+        {
+            const uint32_t vi = tid + 256 * i;
+            if (vi < nvec)
+            {
+                const u32x4 xv = xs[vi];
+#pragma unroll
+                for (int k = 0; k < R; ++k)
+                    acc[k] = dot8(w[k][i], xv, acc[k]);
+            }
+        }
+        if (u + gridDim.x < units)
+            load_unit(u + gridDim.x);
+#pragma unroll
+        for (int k = 0; k < R; ++k)
+            acc[k] = wave_sum_dpp(acc[k]);
+        if (lane == 0)
+#pragma unroll
+            for (int k = 0; k < R; ++k)
+                part[n][wid][k] = acc[k];
+    }
+    __syncthreads();
+    // 4. the rows
+    if (finisher)
+    {
+        const uint32_t n = tid / R, k = tid % R;
+        const float sum = ((part[n][0][k] + part[n][1][k]) + part[n][2][k]) + part[n][3][k];
+        a.out[my_row] = f2h(my_rs + h2f(f2h(sum)));
+    }
+}
+
+template <int R, int NVW> static hipError_t launch_wg_resid(hipStream_t st, const GemvArgs &a, int cu_count)
+{
+    const uint32_t units = (a.rows + R - 1) / R;
+    const size_t lds = (size_t)a.K * 2;
+    static uint64_t occ_memo = 0;
+    const int per_cu = std::max(occupancy_per_cu((const void *)gemv_wg_resid_kernel<R, NVW>, 256, lds, occ_memo), 1);
+    // two workgroups per CU (1, 2 and 3 measure within 2% of each other for the 7B down product), and at most
+    // kWgMaxUnits units per workgroup
+    const uint32_t cap = (uint32_t)(cu_count > 0 ? cu_count : 256) * (uint32_t)std::min(per_cu, 2);
+    const uint32_t grid = std::max(std::min(units, cap), (units + kWgMaxUnits - 1) / kWgMaxUnits);
+    gemv_wg_resid_kernel<R, NVW><<<grid, 256, lds, st>>>(a, units);
+    return hipGetLastError();
+}
+
 // units of R rows for `a`; 0 when R does not fit the epilogue's pairing
 static uint32_t gemv_units(int epi, const GemvArgs &a, int R)
 {
@@ -812,6 +911,19 @@ hipError_t launch_gemv(hipStream_t st, int epi, const GemvArgs &a, int cu_count)
     if (epi == EPI_QKV_ATTN && (R != 2 || a.H > kAttnTailMaxHeads || a.hd % 8 != 0 || a.hd < 32 ||
                                 64 % (a.hd / 8) != 0 || !a.head_count || !a.attn_out))
         return hipErrorInvalidValue;
+    // long rows of the residual product: split over the workgroup's waves (unless a unit size is asked for)
+    if (epi == EPI_RESID && !a.rows_per_unit && nvec > 1024 && nvec <= 2048 && a.resid && a.out)
+        switch ((nvec + 255) / 256)
+        {
+        case 5:
+            return launch_wg_resid<2, 5>(st, a, cu_count);
+        case 6:
+            return launch_wg_resid<2, 6>(st, a, cu_count);
+        case 7:
+            return launch_wg_resid<2, 7>(st, a, cu_count);
+        case 8:
+            return launch_wg_resid<2, 8>(st, a, cu_count);
+        }
     const int NV = (R == 1 || R == 2 || R == 4) ? gemv_pick_nv(R, nvec) : 0;
     if (NV != 0 && (epi != EPI_GATEUP || a.rows % R == 0))
     {
