@@ -291,6 +291,7 @@ template <int NVD, int NVF> __global__ __launch_bounds__(256, 1) void decode_per
                           });
         finish_phase(a, k0);
 
+        // B: attention; the Wo units' weights are requested behind the first cache reads
         wait_barrier(a, k0);
         {
             auto prefetch_wo = [&]() {
