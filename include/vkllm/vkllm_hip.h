@@ -41,8 +41,9 @@ extern vkllm_err_t vkllm_hip_reset_kernel_stats(struct vkllm_context *context);
  * "fused_attn_scores", "fused_attn_pv", "fused_attn_long" (both in one launch), "fused_attn_small", "fused_attn_o"
  * (one-kernel attention and Wo + residual in one launch), "fused_o_resid", "fused_gateup", "fused_down_resid",
  * "fused_logits", "fused_argmax" (the embedding and residual GEMVs write into a scratch row, so repeats leave the
- * model state unchanged), and "decode_step": replays of the captured single-token graph the last step used, at
- * its position. Needs a preceding single-token step of `model`. */
+ * model state unchanged), "decode_step": replays of the captured single-token graph the last step used, at
+ * its position, and "decode_persist": the persistent single-token launch (VKLLM_PERSIST=1) recomputing the last
+ * step, which must have run as that launch. Needs a preceding single-token step of `model`. */
 extern vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *context, struct vkllm_models_llama2 *model,
                                                const char *family, uint32_t reps, uint64_t *total_ns);
 
