@@ -196,7 +196,16 @@ __device__ __forceinline__ void small_block(const AttnDecodeArgs &a, uint32_t h,
     load_keys<U>(k, Kv, k.ks, last, ka, kb);
     load_keys<U>(k, Kv, k.ks + step, last, na, nb);
     after_issue();
+    // the position is read only now, behind the cache rows (the reads above are clamped to small_max): a position
+    // past small_max (the LDS's positions and the speculative loads' bound) is a host error, and the block raises
+    // the step's error flag and writes nothing
     const uint32_t kv = a.step->offset + 1;
+    if (kv > a.small_max)
+    {
+        if (tid == 0 && a.err)
+            __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        return;
+    }
     const uint32_t passes = (kv + rpp - 1) / rpp;
     const uint32_t nit = (kv + step - 1) / step;
     for (uint32_t it = 0; it < nit; ++it)

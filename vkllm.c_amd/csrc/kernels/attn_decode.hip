@@ -384,9 +384,8 @@ __global__ __launch_bounds__(256) void attn_long_kernel(AttnDecodeArgs a)
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// block b of the short-cache attention (blocks of heads >= H do nothing). A position past the launch's small_max
-// (the LDS's positions and the speculative loads' bound) is a host error: the block raises the step's error flag
-// and writes nothing.
+// block b of the short-cache attention (blocks of heads >= H do nothing; a position past the launch's small_max
+// raises the step's error flag, in small_block)
 template <bool AGENT> __device__ __forceinline__ void small_attention(const AttnDecodeArgs &a, uint32_t b, float *sm,
                                                                      float *red)
 {
@@ -394,12 +393,6 @@ template <bool AGENT> __device__ __forceinline__ void small_attention(const Attn
     block_head(b, a.groups, h, g);
     if (h >= a.H)
         return;
-    if (a.step->offset + 1 > a.small_max)
-    {
-        if (threadIdx.x == 0 && a.err)
-            __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        return;
-    }
     small_block<kSmallThreads, AGENT>(a, h, g, sm, red);
 }
 
