@@ -15,7 +15,9 @@
 //                     of each of two 16-key score blocks that it holds)
 // Pass 1 walks all kv positions for M and L (an online sum, rescaled when the row max grows); pass 2 recomputes
 // the same scores (same instructions, same order, so the same fp16 values) for the blocks at or before the last
-// row's position and accumulates P.V. The exponentials are the hardware's (v_exp_f32 on s log2 e - M log2 e) and p
+// row's position and accumulates P.V. Pass 2's first two V blocks are requested at entry and its first two K blocks
+// in pass 1's last step (or, for kv <= 128, read from where pass 1 left them in LDS), so pass 2 starts without a
+// round trip to memory. The exponentials are the hardware's (v_exp_f32 on s log2 e - M log2 e) and p
 // multiplies by 1 / L (the reference's shader leaves exp and the division to the implementation's precision as
 // well). The per-score softmax arithmetic costs more issue cycles than the matrix products, so a block wholly in a
 // wave's future only joins the max, and a block wholly in its past skips the masks.
@@ -75,6 +77,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
     constexpr int KV = kPfKeys * HD / 8 / 256; // 16-byte K vectors per thread per block
     constexpr int VP = 32 * (HD / 8) / 256;    // (key pair, dim chunk) items per thread per block
     constexpr int VT = HD * (kPfKeys / 8) / 256; // transposed rule: (row, key chunk) vectors per thread
+    constexpr int VR = 2 * VP > VT ? 2 * VP : VT; // V registers per set (either layout: 2 VP == VT here)
     // two buffers each of the K tile ([key][dim]) and the V tile ([dim][key]); K buffers first
     extern __shared__ __attribute__((aligned(16))) uint16_t pf_lds[];
     auto Kt = [&](int b) { return pf_lds + b * (kPfKeys * KROW); };
@@ -101,6 +104,35 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
         qf[ks] = *(const f16x8a *)(q + (size_t)rowc * D + (size_t)h * HD + ks * 32 + 8 * q4);
+
+    // V blocks 0 and 1 of pass 2, requested now: they depend on nothing, and pass 2 then starts without a round trip
+    // to memory. Non-transposed, set entries [0, VP) hold keys 2 p and [VP, 2 VP) keys 2 p + 1 of the block (dims
+    // [8 ch, 8 ch + 8)); transposed, entry i holds V row n, dims [jb + 8 c, jb + 8 c + 8) (the tile is read as [n][k]).
+    u32x4 vr[2][VR];
+    auto load_v = [&](auto set_tag, uint32_t jb) {
+        constexpr int SI = decltype(set_tag)::value;
+        if (!transposed)
+        {
+#pragma unroll
+            for (int i = 0; i < VP; ++i)
+            {
+                const uint32_t v = tid + 256 * i, p = v % 32, ch = v / 32;
+                vr[SI][i] = *(const u32x4 *)(Vh + (size_t)min(jb + 2 * p, kv - 1) * HD + ch * 8);
+                vr[SI][VP + i] = *(const u32x4 *)(Vh + (size_t)min(jb + 2 * p + 1, kv - 1) * HD + ch * 8);
+            }
+        }
+        else
+        {
+#pragma unroll
+            for (int i = 0; i < VT; ++i)
+            {
+                const uint32_t v = tid + 256 * i, n = v / (kPfKeys / 8), c = v % (kPfKeys / 8);
+                vr[SI][i] = *(const u32x4 *)(Vh + (size_t)n * HD + min(jb + 8 * c, (uint32_t)HD - 8));
+            }
+        }
+    };
+    load_v(S0{}, 0);
+    load_v(S1{}, kPfKeys);
 
     // Blocks stream through two register sets and the two LDS buffers: while block b is computed from buffer
     // b % 2, set b % 2 loads block b + 2 and set (b + 1) % 2 (block b + 1, requested a block earlier) is stored to
@@ -149,9 +181,18 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
     const uint32_t pos_lo = offset + min(row0 + wave * 16, S - 1), pos_hi = offset + min(row0 + wave * 16 + 15, S - 1);
     float m = -FLT_MAX, l = 0.f;
     const uint32_t nb1 = (kv + kPfKeys - 1) / kPfKeys;
+    // kv <= 2 blocks: pass 1 leaves K blocks 0 and 1 in LDS buffers 0 and 1, where pass 2 reads them; otherwise pass
+    // 1's last step requests them again (both register sets are free by then)
+    const bool reuse_k = nb1 <= 2;
     auto step1 = [&](auto ld, auto cur, auto nxt, int buf, uint32_t jb) {
         if constexpr (decltype(ld)::value >= 1)
             load_k(cur, jb + 2 * kPfKeys);
+        if constexpr (decltype(ld)::value < 0)
+            if (!reuse_k)
+            {
+                load_k(S0{}, 0);
+                load_k(S1{}, kPfKeys);
+            }
         f32x4a st[4];
         scores(buf, st);
         const bool inside = jb + kPfKeys <= kv;
@@ -192,7 +233,8 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
         }
     };
     // LD: the step requests block + 2 (1), only stores the next block (0), or neither (-1): the last two steps of a
-    // pass request nothing past it, so the next pass does not wait behind loads it never uses
+    // pass request nothing past it, so the next pass does not wait behind loads it never uses (pass 1's last step
+    // requests pass 2's first K blocks instead)
     using Ld = std::integral_constant<int, 1>;
     using St = std::integral_constant<int, 0>;
     using Nn = std::integral_constant<int, -1>;
@@ -224,31 +266,6 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
 #pragma unroll
     for (int d = 0; d < DB; ++d)
         o[d] = (f32x4a){0.f, 0.f, 0.f, 0.f};
-    u32x4 va[2][VP], vb[2][VP], vt[2][VT];
-    auto load_v = [&](auto set_tag, uint32_t jb) {
-        constexpr int SI = decltype(set_tag)::value;
-        if (!transposed)
-        {
-            // keys 2 p and 2 p + 1 of the block, dims [8 ch, 8 ch + 8)
-#pragma unroll
-            for (int i = 0; i < VP; ++i)
-            {
-                const uint32_t v = tid + 256 * i, p = v % 32, ch = v / 32;
-                va[SI][i] = *(const u32x4 *)(Vh + (size_t)min(jb + 2 * p, kv - 1) * HD + ch * 8);
-                vb[SI][i] = *(const u32x4 *)(Vh + (size_t)min(jb + 2 * p + 1, kv - 1) * HD + ch * 8);
-            }
-        }
-        else
-        {
-            // V rows n < hd, dims [jb + 8 c, jb + 8 c + 8): the tile is read as [n][k]
-#pragma unroll
-            for (int i = 0; i < VT; ++i)
-            {
-                const uint32_t v = tid + 256 * i, n = v / (kPfKeys / 8), c = v % (kPfKeys / 8);
-                vt[SI][i] = *(const u32x4 *)(Vh + (size_t)n * HD + min(jb + 8 * c, (uint32_t)HD - 8));
-            }
-        }
-    };
     auto store_v = [&](auto set_tag, int buf) {
         constexpr int SI = decltype(set_tag)::value;
         if (!transposed)
@@ -263,8 +280,8 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
                 for (int e = 0; e < 4; ++e)
                 {
                     uint16_t *row = Vt(buf) + (8 * ch + 2 * e) * VROW + col;
-                    *(uint32_t *)row = (va[SI][i][e] & 0xffffu) | (vb[SI][i][e] << 16);
-                    *(uint32_t *)(row + VROW) = (va[SI][i][e] >> 16) | (vb[SI][i][e] & 0xffff0000u);
+                    *(uint32_t *)row = (vr[SI][i][e] & 0xffffu) | (vr[SI][VP + i][e] << 16);
+                    *(uint32_t *)(row + VROW) = (vr[SI][i][e] >> 16) | (vr[SI][VP + i][e] & 0xffff0000u);
                 }
             }
         }
@@ -275,7 +292,7 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
             {
                 const uint32_t v = tid + 256 * i, n = v / (kPfKeys / 8), c = v % (kPfKeys / 8);
                 // units 2c and 2c + 1 trade places in the rows that swizzle ((n >> 3) & 1 = (tid >> 6) & 1)
-                const u32x4 x = vt[SI][i];
+                const u32x4 x = vr[SI][i];
                 *(u32x4 *)(Vt(buf) + n * VROW + 8 * c) = ((tid >> 6) & 1u) ? u32x4{x[2], x[3], x[0], x[1]} : x;
             }
         }
@@ -322,17 +339,16 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
         }
         if constexpr (decltype(ld)::value >= 0)
         {
-            store_k(nxt, buf ^ 1);
+            if (!reuse_k) // nb2 <= nb1, so with reuse_k this is block 1, already in buffer 1
+                store_k(nxt, buf ^ 1);
             store_v(nxt, buf ^ 1);
             __syncthreads();
         }
     };
     const uint32_t nb2e = (nb2 + 1) & ~1u;
-    load_k(S0{}, 0);
-    load_v(S0{}, 0);
-    load_k(S1{}, kPfKeys);
-    load_v(S1{}, kPfKeys);
-    store_k(S0{}, 0);
+    // blocks 0 and 1 are in flight (V since entry, K since pass 1's last step) or, with reuse_k, K is in LDS
+    if (!reuse_k)
+        store_k(S0{}, 0);
     store_v(S0{}, 0);
     __syncthreads();
     for (blk = 0; blk + 2 < nb2e; blk += 2)
