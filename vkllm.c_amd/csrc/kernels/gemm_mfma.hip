@@ -931,7 +931,10 @@ static hipError_t launch_epi_gemm(hipStream_t st, const uint16_t *A, const uint1
         // whole K per tile with four K steps of loads in flight (one workgroup per CU) beats split K and its reduce
         if (M <= 128 && tiles * 3 >= (uint64_t)cus * 2)
             return launch_tile32<128, 128, EPI, false, 4>(st, A, B, C, work, M, N, K, ldc, split, 1, K, 0, rope);
-        const uint64_t per_cu10 = M <= 128 ? 14 : 20; // workgroups per CU, times 10
+        // workgroups per CU, times 10. Plain products above 128 tokens (the MATMUL op's) split K only until one
+        // workgroup per CU runs: a second workgroup per CU leaves the tile kernel no faster and doubles the partials
+        // the reduce reads (M 512, N = K = 4096: 128 tiles x 2 K ranges 29.7 + 5.4 us, x 4 ranges 30.2 + 8.2 us)
+        const uint64_t per_cu10 = M <= 128 ? 14 : EPI == GEMM_PLAIN ? 10 : 20;
         uint32_t splits = 1;
         while (tiles * splits * 2 * 10 <= per_cu10 * cus && K / (splits * 2) >= 256 &&
                (size_t)splits * 2 * M * N <= work_elems)
