@@ -28,9 +28,10 @@ def probe(tmp_path_factory):
                     os.path.join(CSRC, "gguf.cpp"), "-o", exe], check=True)
 
     def run(*paths):
-        env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0:exitcode=23",
+        # the environment is passed on as it is (any preloaded library included); AddressSanitizer is told not to
+        # insist on coming first in the library order
+        env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0:exitcode=23:verify_asan_link_order=0",
                    UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1:exitcode=24")
-        env.pop("LD_PRELOAD", None)
         r = subprocess.run([exe, *map(str, paths)], capture_output=True, text=True, env=env, timeout=60)
         assert r.returncode == 0, f"sanitizer report or crash (exit {r.returncode}):\n{r.stderr[-3000:]}"
         return r.stdout.splitlines()
