@@ -10,8 +10,8 @@
   long-context workload decodes to.
 
 Reference path: src/models/vkllm_llama2_layers.c:98-354 (the layer), :223-257 with src/shaders/vkllm_softmax.comp:42-96
-(the attention), tests/vkllm_test_infer_gguf.c:181-272 (the loop). Bar (one layer, so the north star's): logits within
-2e-2 of the oracle on every row and step; ids equal, except at a one-ulp tie in the oracle's logits (fp32 summation
+(the attention), tests/vkllm_test_infer_gguf.c:181-272 (the loop). Bar (one layer, so fp16 weights with fp32 sums):
+logits within 2e-2 of the oracle on every row and step; ids equal, except at a one-ulp tie in the oracle's logits (fp32 summation
 order alone decides such a row).
 """
 import numpy as np
