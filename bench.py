@@ -4,10 +4,11 @@
 Workloads (--config; the default is the headline one):
   7b       LLaMA-2-7B-shaped decoder (dim 4096, 32 layers, 32 heads of 128, FFN 11008, vocab 32000), a 128-token
            uniform-random prompt prefilled, then greedy decode at batch 1 in a 4096-position KV cache
-  7b-long  the same model, a 1024-token prompt, then 3072 greedy steps (tok/s also reported near positions 1k, 2k
-           and 4k, where attention over the cache grows from 4% to 13% of the bytes)
+  7b-long  the same model, a 1024-token prompt, then greedy decode to position 4095: one untimed step (its graph
+           is captured then), 3070 timed (tok/s also reported near positions 1k, 2k and 4k, where attention over the
+           cache grows from 4% to 13% of the bytes)
   13b      LLaMA-2-13B-shaped decoder (dim 5120, 40 layers, 40 heads of 128, FFN 13824, vocab 32000), a 2048-token
-           prompt, then 128 greedy steps
+           prompt, then 127 greedy steps: two untimed, 125 timed
 fp16 weights are generated on the device from seed 0 (N(0, 0.02), norm weights 1.0); prompt ids from seed 1.
 Every token goes through the library's C API exactly as the reference's driver loop does
 (tests/vkllm_test_infer_gguf.c:181-272): tensor_new(input, mapped) -> graph_new -> models_llama2_build_graph ->
@@ -55,9 +56,9 @@ SHAPE_13B = dict(n_layer=40, dim=5120, n_head=40, ffn=13824, vocab=32000)
 CONFIGS = {
     "7b": dict(shape=SHAPE_7B, prompt=128, steps=256, warmup=8, ctx=4096, name="LLaMA-2-7B-shaped decoder (dim 4096, "
                "32 layers, 32 heads, FFN 11008, vocab 32000), 128-token prompt prefill then greedy decode at batch 1"),
-    "7b-long": dict(shape=SHAPE_7B, prompt=1024, steps=3071, warmup=0, ctx=4096, name="LLaMA-2-7B-shaped decoder, "
+    "7b-long": dict(shape=SHAPE_7B, prompt=1024, steps=3070, warmup=1, ctx=4096, name="LLaMA-2-7B-shaped decoder, "
                     "4096-position KV cache, 1024-token prompt prefill then 3072 greedy steps at batch 1"),
-    "13b": dict(shape=SHAPE_13B, prompt=2048, steps=127, warmup=0, ctx=2304, name="LLaMA-2-13B-shaped decoder "
+    "13b": dict(shape=SHAPE_13B, prompt=2048, steps=125, warmup=2, ctx=2304, name="LLaMA-2-13B-shaped decoder "
                 "(dim 5120, 40 layers, 40 heads, FFN 13824, vocab 32000), 2048-token prompt prefill then 128 greedy "
                 "steps at batch 1"),
 }
@@ -293,9 +294,9 @@ def run_workload(ctx, vk, model, shape, prompt_len, steps, warmup, prefill_reps,
     log(f"decode: {steps} steps in {decode_s:.3f} s = {tps:.1f} tok/s; per step {host}")
     at_positions = {}
     for target in (1024, 2048, 4096):
-        # the 64 timed steps ending at the target position (or starting there when it is the first one),
-        # from the per-step wall times
-        if steps < 64 or not pos0 <= target <= pos + 1:
+        # the 64 timed steps ending at the target position (or the first 64 when the timed steps start at most 8
+        # positions past it, behind the untimed warmup steps), from the per-step wall times
+        if steps < 64 or not pos0 - 8 <= target <= pos + 1:
             continue
         lo = min(max(0, target - pos0 - 64), steps - 64)
         at_positions[str(target)] = round(64 / (float(np.sum(step_ns[lo:lo + 64])) / 1e9), 1)
@@ -336,6 +337,7 @@ def companion(ctx, vk, name, model, prefill_reps, timing_steps):
         "workload": conf["name"],
         "decode_tok_s": round(w["tps"], 2),
         "steps": conf["steps"],
+        "warmup": conf["warmup"],
         "ms_per_step": round(ms, 4),
         "decode_positions": [w["pos0"], w["pos"]],
         "decode_hbm_roofline_frac": round(mean_step_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
