@@ -869,6 +869,9 @@ static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S
     // reading fragment-ordered activations (the normalised rows in xn_t, the attention output in attn_t)
     const bool streamed = fs->stream_ok && S <= 128 && rope_epi && fs->norm_epi;
     uint16_t *xn = streamed ? fs->xn_t : fs->xn;
+    // the streamed vocabulary product stores 4 logits of a row as one 8-byte vector, so its rows of V must stay
+    // 8-byte aligned; otherwise the tile GEMM takes the logits, and the last norm writes its row-major input
+    const bool stream_logits = streamed && V % 4 == 0;
     uint16_t *attn = streamed ? fs->attn_t : fs->attn;
     charge(ctx, fs, NS_ATTN_NORM, 0);
     KTRY(ctx, KID_F_RMSNORM, vk::launch_rmsnorm_rows(st, fs->h, mp->layers[0].attn_norm, xn, S, D, mp->eps, streamed));
@@ -929,7 +932,9 @@ static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S
             charge(ctx, fs, NS_MUL, l);
             KTRY(ctx, KID_F_SWIGLU, vk::launch_swiglu(st, fs->ug, fs->act, S, F));
         }
-        const vk::GemmNorm next_norm{l + 1 < mp->L ? mp->layers[l + 1].attn_norm : mp->out_norm, xn, mp->eps, streamed};
+        const bool last = l + 1 == mp->L;
+        const vk::GemmNorm next_norm{last ? mp->out_norm : mp->layers[l + 1].attn_norm,
+                                     last && !stream_logits ? fs->xn : xn, mp->eps, last ? stream_logits : streamed};
         charge(ctx, fs, NS_DOWN, l);
         KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_RESID, fs->act, ly.wd, fs->h, S, D, F, D, 0, cu, fs->gemm_work, kGemmWorkElems, nullptr, fs->norm_epi ? &next_norm : nullptr));
         if (!fs->norm_epi)
@@ -942,8 +947,7 @@ static vkllm_err_t enqueue_prefill(vkllm_context *ctx, ModelPriv *mp, uint32_t S
         }
     }
     charge(ctx, fs, NS_LOGITS);
-    // the streamed product stores 4 logits of a row as one 8-byte vector, so its rows of V must stay 8-byte aligned
-    if (streamed && V % 4 == 0)
+    if (stream_logits)
         KTRY(ctx, KID_F_GEMM, stream_product(st, fs, vk::STREAM_PLAIN, xn, fs->out_t, fs->logits, S, V, D, V));
     else
         KTRY(ctx, KID_F_GEMM, vk::launch_gemm(st, vk::GEMM_PLAIN, fs->xn, mp->out_w, fs->logits, S, V, D, V, 0, cu, fs->gemm_work, kGemmWorkElems));
