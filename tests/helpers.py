@@ -84,3 +84,39 @@ def assert_prefill_ids(ids, want_ids, want_logits, what=""):
     if ties:
         print(f"{what}: {ties} of {len(ids)} rows took the other id of a one-ulp tie")
     return ties
+
+
+def prompt_rows(ref, model, part, offset, what, tol=2e-2):
+    """One prompt step of `part` at `offset` on the oracle and the library: every row's logits within tol, ids as
+    assert_prefill_ids takes them. Returns the oracle's ids and the number of one-ulp ties."""
+    print(f"[{what}] prompt rows {offset}..{offset + len(part) - 1}", flush=True)
+    want_ids, want_logits, _ = ref.step(part, offset, want_logits=True)
+    ids = model.step(part, offset)
+    logits = model.last_logits(len(part)).astype(np.float32)
+    err = float(np.max(np.abs(logits - want_logits.astype(np.float32))))
+    print(f"[{what}] rows {offset}..{offset + len(part) - 1}: max|dlogit| {err:.3g}", flush=True)
+    assert err <= tol
+    ties = assert_prefill_ids(ids, want_ids, want_logits, f"{what} rows at {offset}")
+    return want_ids, ties
+
+
+def forced_decode(ref, model, first_tok, offset, n, what, tol=2e-2):
+    """n single-token steps from position `offset`, each fed the oracle's previous id; returns the worst logit
+    difference, the number of one-ulp ties and the oracle's last id (the next step's input)."""
+    tok, worst, ties = int(first_tok), 0.0, 0
+    for i in range(n):
+        toks = np.array([tok], np.uint32)
+        want_ids, want_logits, _ = ref.step(toks, offset + i, want_logits=True)
+        ids = model.step(toks, offset + i)
+        logits = model.last_logits(1).astype(np.float32)
+        err = float(np.max(np.abs(logits - want_logits.astype(np.float32))))
+        worst = max(worst, err)
+        assert err <= tol, f"{what} position {offset + i}: max|dlogit| {err}"
+        a, b = int(ids[0]), int(want_ids[0])
+        if a != b:
+            row = want_logits[0].astype(np.float32)
+            assert row[b] - row[a] <= float(fp16_ulp(row[b])), f"{what} position {offset + i}: id {a} vs {b}"
+            ties += 1
+        tok = b
+    print(f"[{what}] decode {offset}..{offset + n - 1}: max|dlogit| {worst:.3g}, {ties} one-ulp ties", flush=True)
+    return worst, ties, tok

@@ -17,7 +17,7 @@ order alone decides such a row).
 import numpy as np
 import pytest
 
-from helpers import assert_prefill_ids, fp16_ulp
+from helpers import forced_decode, prompt_rows
 
 pytestmark = pytest.mark.gpu
 
@@ -32,49 +32,15 @@ def _models(oracle, vk, ctx, shape, seed):
     return cfg, ref, vk.Model(ctx, config=vcfg, seed=seed)
 
 
-def _prompt_chunk(ref, model, part, offset, what):
-    print(f"[{what}] prompt rows {offset}..{offset + len(part) - 1}", flush=True)
-    want_ids, want_logits, _ = ref.step(part, offset, want_logits=True)
-    ids = model.step(part, offset)
-    logits = model.last_logits(len(part)).astype(np.float32)
-    err = float(np.max(np.abs(logits - want_logits.astype(np.float32))))
-    print(f"[{what}] rows {offset}..{offset + len(part) - 1}: max|dlogit| {err:.3g}", flush=True)
-    assert err <= LOGIT_TOL
-    ties = assert_prefill_ids(ids, want_ids, want_logits, f"{what} rows at {offset}")
-    return want_ids, ties
-
-
-def _forced_decode(ref, model, first_tok, offset, n, what):
-    """n single-token steps from position `offset`, each fed the oracle's previous id; returns the worst logit
-    difference, the number of one-ulp ties and the oracle's last id (the next step's input)."""
-    tok, worst, ties = int(first_tok), 0.0, 0
-    for i in range(n):
-        toks = np.array([tok], np.uint32)
-        want_ids, want_logits, _ = ref.step(toks, offset + i, want_logits=True)
-        ids = model.step(toks, offset + i)
-        logits = model.last_logits(1).astype(np.float32)
-        err = float(np.max(np.abs(logits - want_logits.astype(np.float32))))
-        worst = max(worst, err)
-        assert err <= LOGIT_TOL, f"{what} position {offset + i}: max|dlogit| {err}"
-        a, b = int(ids[0]), int(want_ids[0])
-        if a != b:
-            row = want_logits[0].astype(np.float32)
-            assert row[b] - row[a] <= float(fp16_ulp(row[b])), f"{what} position {offset + i}: id {a} vs {b}"
-            ties += 1
-        tok = b
-    print(f"[{what}] decode {offset}..{offset + n - 1}: max|dlogit| {worst:.3g}, {ties} one-ulp ties", flush=True)
-    return worst, ties, tok
-
-
 @pytest.mark.timeout(600)  # the oracle's 2048-token step at the 13B widths runs on the host's cores
 def test_13b_widths_2048_token_prompt(ctx, vk, oracle):
     shape = dict(n_layer=1, dim=5120, n_head=40, ffn=13824, vocab=1000, ctx=2176)
     cfg, ref, model = _models(oracle, vk, ctx, shape, seed=61)
     try:
         prompt = oracle.prompt_tokens(62, 2048, cfg.vocab)
-        want_ids, ties = _prompt_chunk(ref, model, prompt, 0, "13b 2048")
+        want_ids, ties = prompt_rows(ref, model, prompt, 0, "13b 2048", LOGIT_TOL)
         assert ties <= 2048 // 100
-        _, ties, _ = _forced_decode(ref, model, want_ids[-1], 2048, 8, "13b 2048")
+        _, ties, _ = forced_decode(ref, model, want_ids[-1], 2048, 8, "13b 2048", LOGIT_TOL)
         assert ties <= 1
     finally:
         ref.close()
@@ -89,7 +55,7 @@ def test_7b_widths_decode_to_4096_positions(ctx, vk, oracle):
         prompt = oracle.prompt_tokens(72, 4000, cfg.vocab)
         offset, ties = 0, 0
         for n in (1024, 1024, 1024, 928):
-            want_ids, t = _prompt_chunk(ref, model, prompt[offset:offset + n], offset, "7b 4096")
+            want_ids, t = prompt_rows(ref, model, prompt[offset:offset + n], offset, "7b 4096", LOGIT_TOL)
             ties += t
             offset += n
         assert ties <= 4000 // 100
@@ -97,11 +63,11 @@ def test_7b_widths_decode_to_4096_positions(ctx, vk, oracle):
         # kernel counts show that every one of them took the one-launch long-cache attention
         last = 8
         n = shape["ctx"] - offset - last
-        _, ties, tok = _forced_decode(ref, model, want_ids[-1], offset, n, "7b 4096")
+        _, ties, tok = forced_decode(ref, model, want_ids[-1], offset, n, "7b 4096", LOGIT_TOL)
         ctx.set_timing(True)
         ctx.reset_kernel_stats()
         try:
-            _, t2, _ = _forced_decode(ref, model, tok, offset + n, last, "7b 4096 timed")
+            _, t2, _ = forced_decode(ref, model, tok, offset + n, last, "7b 4096 timed", LOGIT_TOL)
             stats = ctx.kernel_stats()
         finally:
             ctx.set_timing(False)
