@@ -101,3 +101,30 @@ def test_switch_changes_no_result(ctx, vk, oracle, monkeypatch):
             print(f"step {i}: oracle margin {top2[1] - top2[0]:.4f}; streams compared up to it")
             break
         assert a == b, f"step {i}: id {a} vs oracle {b} at margin {top2[1] - top2[0]:.4f}"
+
+
+def test_two_models_interleaved(ctx, vk, oracle):
+    """Two models of different widths on one context, their greedy steps interleaved: each model's step launched
+    ahead runs (stream order) while the other model's call is served, and is taken when its own next call matches.
+    Every step of both against its own oracle."""
+    cfg_a, ref_a, model_a = _pair(oracle, vk, ctx, seed=85)
+    cfg_b = oracle.make_cfg(n_layer=2, dim=192, n_head=3, ffn=384, vocab=777, ctx=64)
+    ref_b = oracle.Model(cfg=cfg_b, seed=86)
+    model_b = vk.Model(ctx, config=vk.llama_config(2, 192, 3, 384, 777, 64), seed=86)
+    try:
+        nxt_a = _check(ref_a, model_a, oracle.prompt_tokens(87, 12, cfg_a.vocab), 0, "prompt a")
+        nxt_b = _check(ref_b, model_b, oracle.prompt_tokens(88, 9, cfg_b.vocab), 0, "prompt b")
+        pos_a, pos_b = 12, 9
+        for i in range(10):
+            nxt_a = _check(ref_a, model_a, [nxt_a], pos_a, f"a at {pos_a}")
+            nxt_b = _check(ref_b, model_b, [nxt_b], pos_b, f"b at {pos_b}")
+            pos_a, pos_b = pos_a + 1, pos_b + 1
+            if i % 3 == 2:  # now and then two steps of one model in a row
+                nxt_a = _check(ref_a, model_a, [nxt_a], pos_a, f"a again at {pos_a}")
+                pos_a += 1
+        print("[ahead] two models interleaved: every step matched its oracle", flush=True)
+    finally:
+        ref_a.close()
+        ref_b.close()
+        model_a.close()
+        model_b.close()

@@ -93,3 +93,25 @@ def test_shape_against_oracle(ctx, vk, oracle, name):
     finally:
         ref.close()
         model.close()
+
+
+def test_decode_to_the_last_cache_position_then_past_it(ctx, vk, oracle):
+    """Decode up to the cache's last position (no step is launched ahead past it) against the oracle; a step at the
+    position after it, or a prompt that would run past it, is refused with VKLLM_ERR_ARGS and leaves the model usable
+    (the reference's build_graph bounds the cache view the same way, src/models/vkllm_kvcache.c:12-124)."""
+    shape = _shape(256, 4, 512, ctx=48)
+    ref = oracle.Model(cfg=oracle.make_cfg(**shape), seed=93)
+    model = vk.Model(ctx, config=vk.llama_config(2, 256, 4, 512, 1000, 48), seed=93)
+    try:
+        prompt = oracle.prompt_tokens(94, 20, 1000)
+        want_ids, _ = prompt_rows(ref, model, prompt, 0, "to ctx", LOGIT_TOL)
+        _, _, tok = forced_decode(ref, model, want_ids[-1], 20, 28, "to ctx", LOGIT_TOL)  # positions 20..47
+        for toks, at in (([tok], 48), ([tok, tok], 47), ([1] * 30, 20)):
+            with pytest.raises(vk.VkllmError) as e:
+                model.step(np.array(toks, np.uint32), at)
+            assert e.value.code == vk.ERR_ARGS, e.value
+        # still usable: the last position again, as the oracle computes it
+        forced_decode(ref, model, tok, 47, 1, "to ctx again", LOGIT_TOL)
+    finally:
+        ref.close()
+        model.close()
