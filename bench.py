@@ -29,6 +29,9 @@ Printed (one JSON line on stdout):
                measured after the headline one in the same process, through the same C loop and with their own step
                counts whatever --steps says: their decode tok/s, tok/s near positions 1k/2k/4k, prefill ms, and HBM
                roofline fractions
+  device_floors  the HBM read rate of a kernel that only streams bytes (at 192 MiB and 1 GiB) and the cost of one
+               dependent, graph-replayed launch of an empty kernel, measured on the same GPU; and the decode step's
+               bytes per second as a fraction of that read rate
   isolated_kernels  (--config 7b, no --no-isolated; alone with --isolated-only) the isolated operators through the
                public VKLLM_OP_* API: GEMV [1x4096].[4096x11008] and [1x4096].[4096x32000], GEMM
                [512x4096].[4096x4096], RMSNorm [512x4096], RoPE [1,32,512,128]; average launch duration back to back
@@ -181,6 +184,25 @@ def cpu_baseline(shape, seconds):
                   f"in {el:.1f} s on {cores} host threads; model built from seed {MODEL_SEED} in {t_build:.0f} s "
                   f"(not timed)",
     }
+
+
+def device_floors(ctx):
+    """What this GPU does with kernels that do nothing else (vkllm_hip_probe_stream_read / _launch_gap): the HBM read
+    rate of a kernel that only streams bytes (non-temporal 16-byte loads, each byte once, windows of a 1 GiB buffer so
+    none is found in the 256 MB memory-side cache), at a decode product's size (192 MiB, gate/up is 172 MiB) and at
+    1 GiB; and the time per launch of a graph-replayed chain of empty kernels (one workgroup, and 1024), the cost of
+    one kernel boundary of the decode step."""
+    out = {}
+    for mib in (192, 1024):
+        med, best = ctx.probe_stream_read(mib << 20, 16)
+        out[f"stream_read_{mib}MiB"] = {"median_GBps": round(med, 1), "best_GBps": round(best, 1),
+                                         "frac_of_peak": round(med / HBM_PEAK_GBS, 4)}
+        log(f"  stream read of {mib} MiB windows: median {med:.0f} GB/s, best {best:.0f} GB/s")
+    for blocks in (1, 1024):
+        us = ctx.probe_launch_gap(256, blocks)
+        out[f"launch_gap_us_{blocks}wg"] = round(us, 3)
+        log(f"  dependent launch of an empty kernel ({blocks} workgroups), graph-replayed: {us:.2f} us")
+    return out
 
 
 def isolated_kernels(ctx, vk, reps=64):
@@ -391,10 +413,11 @@ def main():
     if args.isolated_only:
         log(f"device {ctx.arch()}; isolated operators")
         iso = isolated_kernels(ctx, vk)
+        floors = device_floors(ctx)
         ctx.close()
         print(json.dumps({"metric": "isolated operator kernels, fp16 operands, fp32 accumulation", "n_gpus": 1,
                           "dtype": "f16 storage, f32 accumulate", "data": "synthetic: N(0,1) operands, fixed seeds",
-                          "isolated_kernels": iso}), flush=True)
+                          "isolated_kernels": iso, "device_floors": floors}), flush=True)
         return
     if args.copy_calibration > 0:
         copy_calibration(ctx, vk, args.copy_calibration)
@@ -484,6 +507,11 @@ def main():
     result["isolated_kernels"] = None
     if not args.no_isolated and args.config == "7b":
         result["isolated_kernels"] = isolated_kernels(ctx, vk)
+    # the device's streaming-read rate and kernel-boundary cost, against which the decode step is read as well
+    floors = device_floors(ctx)
+    floors["decode_step_frac_of_stream_read_1024MiB"] = round(
+        mean_step_bytes / (decode_s / steps) / 1e9 / floors["stream_read_1024MiB"]["median_GBps"], 4)
+    result["device_floors"] = floors
     ctx.close()
     if args.cpu_seconds > 0:
         log(f"cpu baseline (oracle, full depth, {oracle_threads()} threads)")

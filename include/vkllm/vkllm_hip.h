@@ -54,6 +54,20 @@ extern vkllm_err_t vkllm_hip_model_time_kernel(struct vkllm_context *context, st
 extern vkllm_err_t vkllm_hip_time_ops(struct vkllm_context *context, struct vkllm_tensor *const *tensors, uint32_t n,
                                       uint32_t reps, uint64_t *total_ns);
 
+/* Device figures for reading the roofline fractions (no counterpart in the reference; measurement entry points).
+ * vkllm_hip_probe_stream_read: the HBM read rate, in GB/s (1e9 bytes per second), of a kernel that only streams
+ * `window_bytes` with 16-byte non-temporal loads (each byte read once, nothing written), over windows of a 1 GiB
+ * buffer that the call allocates and frees, so no window is found in the 256 MB memory-side cache; the median and
+ * the best of `reps` timed passes (1..1024) after an untimed one. window_bytes is a multiple of 32 MiB, at most
+ * 1 GiB.
+ * vkllm_hip_probe_launch_gap: microseconds per launch of a chain of `launches` (1..4096) empty kernels of `blocks`
+ * workgroups of 256 threads, each after the one before on the context's stream, captured into a hipGraph and
+ * replayed as the decode step is: the cost of one kernel boundary. */
+extern vkllm_err_t vkllm_hip_probe_stream_read(struct vkllm_context *context, uint64_t window_bytes, uint32_t reps,
+                                               double *gbps_median, double *gbps_best);
+extern vkllm_err_t vkllm_hip_probe_launch_gap(struct vkllm_context *context, uint32_t launches, uint32_t blocks,
+                                              double *us_per_launch);
+
 /* Model configuration for vkllm_models_llama2_init_random. */
 struct vkllm_llama2_config
 {

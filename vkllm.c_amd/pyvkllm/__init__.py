@@ -207,6 +207,9 @@ def lib():
             "vkllm_hip_synchronize": (E, [vp]),
             "vkllm_hip_context_stream": (E, [vp, ctypes.POINTER(vp)]),
             "vkllm_hip_time_ops": (E, [vp, ctypes.POINTER(TensorP), u32, u32, ctypes.POINTER(ctypes.c_uint64)]),
+            "vkllm_hip_probe_stream_read": (E, [vp, ctypes.c_uint64, u32, ctypes.POINTER(ctypes.c_double),
+                                                ctypes.POINTER(ctypes.c_double)]),
+            "vkllm_hip_probe_launch_gap": (E, [vp, u32, u32, ctypes.POINTER(ctypes.c_double)]),
             "vkllm_hip_kernel_stats": (E, [vp, E, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_uint64),
                                            ctypes.POINTER(ctypes.c_uint64)]),
             "vkllm_hip_reset_kernel_stats": (E, [vp]),
@@ -353,6 +356,20 @@ class Ctx:
         ns = ctypes.c_uint64()
         check("vkllm_hip_time_ops", lib().vkllm_hip_time_ops(self.vp, arr, len(tensors), reps, ctypes.byref(ns)))
         return ns.value
+
+    def probe_stream_read(self, window_bytes, reps):
+        """(median, best) GB/s of a kernel that only streams window_bytes from HBM (vkllm_hip_probe_stream_read)."""
+        med, best = ctypes.c_double(), ctypes.c_double()
+        check("vkllm_hip_probe_stream_read", lib().vkllm_hip_probe_stream_read(self.vp, window_bytes, reps,
+                                                                                ctypes.byref(med), ctypes.byref(best)))
+        return med.value, best.value
+
+    def probe_launch_gap(self, launches, blocks):
+        """Microseconds per launch of a graph-replayed chain of empty kernels (vkllm_hip_probe_launch_gap)."""
+        us = ctypes.c_double()
+        check("vkllm_hip_probe_launch_gap", lib().vkllm_hip_probe_launch_gap(self.vp, launches, blocks,
+                                                                              ctypes.byref(us)))
+        return us.value
 
     def reset_kernel_stats(self):
         check("vkllm_hip_reset_kernel_stats", lib().vkllm_hip_reset_kernel_stats(self.vp))
