@@ -172,13 +172,18 @@ struct NoHook
     __device__ void operator()() const {}
 };
 // after_issue runs once the block's first keys and V rows are requested (the persistent step requests the next
-// product's weights there, behind the cache reads)
-template <int NT, bool AGENT, typename Hook = NoHook>
+// product's weights there, behind the cache reads).
+// UK: key rows per thread in a batch (kpp UK keys per batch); NB: batches of keys requested before the position is
+// read (2: the second is requested during the first's scores otherwise); VPRE: passes of V rows requested then.
+// The launcher sizes them to the launch's bound small_max, so that a short cache asks for no more rows than it can
+// hold (a row past small_max would only repeat the clamped last one).
+template <int NT, bool AGENT, typename Hook = NoHook, int UK = 4, int NB = 2, int VPRE = 2>
 __device__ __forceinline__ void small_block(const AttnDecodeArgs &a, uint32_t h, uint32_t g, float *sm, float *red,
                                             Hook after_issue = Hook())
 {
+    static_assert(UK >= 1 && UK <= 4 && (NB == 1 || NB == 2) && (VPRE == 1 || VPRE == 2), "speculative sizes");
     constexpr uint32_t NW = NT / 64;
-    constexpr int U = 4, UV = kSmallMaxPasses;
+    constexpr int U = UK, UV = kSmallMaxPasses;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t dg = a.hd / a.groups, d0 = g * dg, vpr = a.hd / 8, last = min(a.small_max, a.ctx) - 1;
     // V layout: lane = (vector vl of the slice, row slot); a wave covers seg rows, the block rpp rows per pass
@@ -188,13 +193,15 @@ __device__ __forceinline__ void small_block(const AttnDecodeArgs &a, uint32_t h,
     const u32x4 *Vv = (const u32x4 *)Vh + d0 / 8 + vl;
     u32x4 vv[UV];
     vv[0] = Vv[(size_t)min(vs, last) * vpr];
-    vv[1] = Vv[(size_t)min(vs + rpp, last) * vpr];
+    if constexpr (VPRE > 1)
+        vv[1] = Vv[(size_t)min(vs + rpp, last) * vpr];
     const KeyLayout k = key_layout<NT>(a.q + (size_t)h * a.hd, a.hd);
     const u32x4 *Kv = (const u32x4 *)(a.kc + (size_t)h * a.ctx * a.hd);
     const uint32_t step = k.kpp * U;
     u32x4 ka[U], kb[U], na[U], nb[U];
     load_keys<U>(k, Kv, k.ks, last, ka, kb);
-    load_keys<U>(k, Kv, k.ks + step, last, na, nb);
+    if constexpr (NB > 1)
+        load_keys<U>(k, Kv, k.ks + step, last, na, nb);
     after_issue();
     // the position is read only now, behind the cache rows (the reads above are clamped to small_max): a position
     // past small_max (the LDS's positions and the speculative loads' bound) is a host error, and the block raises
@@ -210,19 +217,25 @@ __device__ __forceinline__ void small_block(const AttnDecodeArgs &a, uint32_t h,
     const uint32_t nit = (kv + step - 1) / step;
     for (uint32_t it = 0; it < nit; ++it)
     {
+        const bool more = it + 1 < nit; // block-uniform
+        if constexpr (NB == 1)
+            if (more)
+                load_keys<U>(k, Kv, k.ks + (it + 1) * step, kv - 1, na, nb);
         score_keys<U>(k, ka, kb, k.ks + it * step, kv, a.scale, sm);
+        if (more)
 #pragma unroll
-        for (int u = 0; u < U; ++u)
-        {
-            ka[u] = na[u];
-            kb[u] = nb[u];
-        }
-        if (it + 2 < nit)
-            load_keys<U>(k, Kv, k.ks + (it + 2) * step, kv - 1, na, nb);
+            for (int u = 0; u < U; ++u)
+            {
+                ka[u] = na[u];
+                kb[u] = nb[u];
+            }
+        if constexpr (NB > 1)
+            if (it + 2 < nit)
+                load_keys<U>(k, Kv, k.ks + (it + 2) * step, kv - 1, na, nb);
     }
-    // V rows past the first two passes (kv > 2 rpp) once the key registers are free
+    // V rows past the passes requested at the start, once the key registers are free
 #pragma unroll
-    for (int t = 2; t < UV; ++t)
+    for (int t = VPRE; t < UV; ++t)
         if ((uint32_t)t < passes)
             vv[t] = Vv[(size_t)min(vs + rpp * t, kv - 1) * vpr];
     __syncthreads();

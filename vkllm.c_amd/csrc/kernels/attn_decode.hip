@@ -386,21 +386,22 @@ __global__ __launch_bounds__(256) void attn_long_kernel(AttnDecodeArgs a)
 // ---------------------------------------------------------------------------------------------------------------
 // block b of the short-cache attention (blocks of heads >= H do nothing; a position past the launch's small_max
 // raises the step's error flag, in small_block)
-template <bool AGENT> __device__ __forceinline__ void small_attention(const AttnDecodeArgs &a, uint32_t b, float *sm,
-                                                                     float *red)
+template <bool AGENT, int UK = 4, int NB = 2, int VPRE = 2>
+__device__ __forceinline__ void small_attention(const AttnDecodeArgs &a, uint32_t b, float *sm, float *red)
 {
     uint32_t h, g;
     block_head(b, a.groups, h, g);
     if (h >= a.H)
         return;
-    small_block<kSmallThreads, AGENT>(a, h, g, sm, red);
+    small_block<kSmallThreads, AGENT, NoHook, UK, NB, VPRE>(a, h, g, sm, red);
 }
 
+template <int UK, int NB, int VPRE>
 __global__ __launch_bounds__(kSmallThreads) void attn_decode_small_kernel(AttnDecodeArgs a)
 {
     extern __shared__ float sm[];
     __shared__ float red[kSmallRed];
-    small_attention<false>(a, blockIdx.x, sm, red);
+    small_attention<false, UK, NB, VPRE>(a, blockIdx.x, sm, red);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -607,7 +608,49 @@ hipError_t launch_attn_small(hipStream_t st, const AttnDecodeArgs &a, uint32_t k
         return hipErrorInvalidValue;
     AttnDecodeArgs b = a;
     b.small_max = kv_max;
-    attn_decode_small_kernel<<<small_blocks(a), kSmallThreads, (size_t)kv_max * sizeof(float), st>>>(b);
+    // the keys and V rows requested before the position is known, sized to kv_max: per batch of keys a thread takes
+    // UK rows kpp apart (one batch when kv_max <= 4 kpp, else two, the rest later); V passes of rpp rows (two at
+    // most). Measured at the 7B widths and kv 150 (bucket bound 192): 128 KB of key rows per block requested, 38 KB
+    // of them live, with the fixed two batches of four.
+    uint32_t lpk = 1;
+    while (lpk * 16 < a.hd)
+        lpk <<= 1;
+    const uint32_t kpp = kSmallThreads / lpk, dg = a.hd / a.groups, rpp = (kSmallThreads / 64) * (64 / (dg / 8));
+    const uint32_t uk = (kv_max + kpp - 1) / kpp, vpre = (kv_max + rpp - 1) / rpp;
+    const dim3 grid(small_blocks(a));
+    const size_t lds = (size_t)kv_max * sizeof(float);
+    if (uk > 4)
+        attn_decode_small_kernel<4, 2, 2><<<grid, kSmallThreads, lds, st>>>(b);
+    else if (vpre > 1)
+        switch (uk)
+        {
+        case 1:
+            attn_decode_small_kernel<1, 1, 2><<<grid, kSmallThreads, lds, st>>>(b);
+            break;
+        case 2:
+            attn_decode_small_kernel<2, 1, 2><<<grid, kSmallThreads, lds, st>>>(b);
+            break;
+        case 3:
+            attn_decode_small_kernel<3, 1, 2><<<grid, kSmallThreads, lds, st>>>(b);
+            break;
+        default:
+            attn_decode_small_kernel<4, 1, 2><<<grid, kSmallThreads, lds, st>>>(b);
+        }
+    else
+        switch (uk)
+        {
+        case 1:
+            attn_decode_small_kernel<1, 1, 1><<<grid, kSmallThreads, lds, st>>>(b);
+            break;
+        case 2:
+            attn_decode_small_kernel<2, 1, 1><<<grid, kSmallThreads, lds, st>>>(b);
+            break;
+        case 3:
+            attn_decode_small_kernel<3, 1, 1><<<grid, kSmallThreads, lds, st>>>(b);
+            break;
+        default:
+            attn_decode_small_kernel<4, 1, 1><<<grid, kSmallThreads, lds, st>>>(b);
+        }
     return hipGetLastError();
 }
 
