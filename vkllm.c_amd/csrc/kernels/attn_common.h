@@ -171,6 +171,14 @@ struct NoHook
 {
     __device__ void operator()() const {}
 };
+// exp(x) as 2^(x log2 e) on the hardware exponential (v_exp_f32), as the prompt-step attention takes it (the
+// reference's shader leaves exp to the implementation's precision); a block's softmax then costs a few cycles per
+// score instead of the library expf's range reduction and polynomial
+__device__ __forceinline__ float small_exp(float x)
+{
+    return __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+}
+
 // after_issue runs once the block's first keys and V rows are requested (the persistent step requests the next
 // product's weights there, behind the cache reads).
 // UK: key rows per thread in a batch (kpp UK keys per batch); NB: batches of keys requested before the position is
@@ -246,14 +254,14 @@ __device__ __forceinline__ void small_block(const AttnDecodeArgs &a, uint32_t h,
     M = wave_max_dpp(M);
     float L = 0.f;
     for (uint32_t j = lane; j < kv; j += 64)
-        L += expf(sm[j] - M);
+        L += small_exp(sm[j] - M);
     L = wave_sum_dpp(L);
     uint16_t *out = a.out + (size_t)h * a.hd + d0;
     if (kv == a.hd)
     {
         __syncthreads(); // every wave has its statistics before the scores become probabilities
         for (uint32_t j = tid; j < kv; j += NT)
-            sm[j] = h2f(f2h(expf(sm[j] - M) / L));
+            sm[j] = h2f(f2h(small_exp(sm[j] - M) / L));
         __syncthreads();
         pv_transposed_pairs<AGENT>(sm, Vh, out, kv, a.hd, d0, dg);
         return;
@@ -266,7 +274,7 @@ __device__ __forceinline__ void small_block(const AttnDecodeArgs &a, uint32_t h,
         if ((uint32_t)t < passes) // block-uniform
         {
             const bool live = j < kv;
-            const float pj = live ? h2f(f2h(expf(sm[min(j, kv - 1)] - M) / L)) : 0.f;
+            const float pj = live ? h2f(f2h(small_exp(sm[min(j, kv - 1)] - M) / L)) : 0.f;
 #pragma unroll
             for (int e = 0; e < 4; ++e)
             {
