@@ -7,8 +7,9 @@ in vkllm.c_amd/csrc/fused.cpp):
   * prompt length: one token (the decode kernels at position 0), two tokens, up to 32 tokens (the streamed QKV
     product split over K with the RoPE reduce), 33-128 tokens (the QKV product split over tokens), 129 tokens (the
     tile GEMMs), and prompts in chunks at nonzero offsets;
-  * head size 32, 48 (no RoPE epilogue, no streamed products), 64 and 128 (the transposed P.V when the cache holds
-    exactly head_dim positions), and head counts that are not multiples of 8;
+  * head size 8, 16, 32, 48 (no RoPE epilogue, no streamed products), 64, 128 and 256 (the transposed P.V when the
+    cache holds exactly head_dim positions, in a prompt step and in a decode step), and head counts that are not
+    multiples of 8; head size 256 past the short-cache bound (768 positions there) takes the two-kernel attention;
   * FFN widths that are multiples of 32, of 16 only (no fused SwiGLU epilogue on the tile GEMM), of 8 only (no
     streamed products), and of 4 only (node-by-node execution through the VKLLM_OP_* kernels);
   * vocabularies that are not multiples of 4.
@@ -45,6 +46,12 @@ CASES = {
     "hd32-3heads": (_shape(96, 3, 256, vocab=500), [40], 6),
     "hd48-6heads": (_shape(288, 6, 768), [20], 6),
     "hd128-3heads-through-kv128": (_shape(384, 3, 1024), [50], 90),
+    # head_dim 256: a first prompt of exactly 256 positions (the transposed P.V in the prompt step), a second chunk at
+    # offset 256, then decode past the short-cache bound of 768 positions on the two-kernel attention
+    "hd256-2heads-past-768": (_shape(512, 2, 1024, ctx=800), [256, 504], 20),
+    # head_dim 16 and 8: decode through kv == head_dim, and a prompt of exactly head_dim positions
+    "hd16-4heads-through-kv16": (_shape(64, 4, 128, vocab=300), [10], 12),
+    "hd8-8heads-prompt8": (_shape(64, 8, 128, vocab=300), [8], 6),
     "ffn528-prompt60": (_shape(256, 4, 528), [60], 4),
     "ffn528-prompt150": (_shape(256, 4, 528), [150], 4),
     "ffn520-prompt60": (_shape(256, 4, 520), [60], 4),

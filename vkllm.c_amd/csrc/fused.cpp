@@ -414,6 +414,8 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         shape.H = mp->H;
         shape.hd = mp->hd;
         shape.ctx = mp->ctx;
+        shape.cmax = fs->att_cmax;
+        shape.chunk = fs->att_chunk;
         const char *ag = getenv("VKLLM_ATTN_GROUPS");
         fs->attn_max_groups = ag && *ag ? (uint32_t)strtoul(ag, nullptr, 10) : 8u;
         shape.groups = vk::attn_groups(mp->H, mp->hd, fs->attn_max_groups);
@@ -450,7 +452,8 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
             HIP_TRY(hipMemset(fs->persist_sync, 0, vk::kPersistSyncWords * sizeof(uint32_t)));
         }
         const char *al = getenv("VKLLM_ATTN_LONG");
-        fs->attn_long = !(al && *al == '0');
+        // head_dim 256 (or chunks shorter than head_dim) takes the two-kernel attention past the short-cache bound
+        fs->attn_long = !(al && *al == '0') && vk::attn_long_ok(shape);
         const char *re = getenv("VKLLM_ROPE_EPI");
         fs->rope_epi = !(re && *re == '0');
         const char *ne = getenv("VKLLM_NORM_EPI");

@@ -569,12 +569,17 @@ hipError_t launch_attn_pv(hipStream_t st, const AttnDecodeArgs &a)
     return hipGetLastError();
 }
 
-hipError_t launch_attn_long(hipStream_t st, const AttnDecodeArgs &a, int cu_count)
+bool attn_long_ok(const AttnDecodeArgs &a)
 {
     // one round trip of keys and of V rows per block (head_dim <= 128 with chunks of <= 256 positions); the
     // transposed product (kv == hd) fits one chunk
-    if (!attn_args_ok(a) || a.hd > 128 || a.cmax == 0 || a.chunk == 0 || a.chunk > 256 || a.chunk < a.hd ||
-        (uint64_t)a.chunk * a.cmax < a.ctx || a.cmax > 256 || !a.part || !a.stats || !a.long_sync || !a.err)
+    return attn_args_ok(a) && a.hd <= 128 && a.cmax > 0 && a.chunk >= a.hd && a.chunk <= 256 &&
+           (uint64_t)a.chunk * a.cmax >= a.ctx && a.cmax <= 256;
+}
+
+hipError_t launch_attn_long(hipStream_t st, const AttnDecodeArgs &a, int cu_count)
+{
+    if (!attn_long_ok(a) || a.chunk == 0 || !a.part || !a.stats || !a.long_sync || !a.err)
         return hipErrorInvalidValue;
     const size_t lds = (size_t)a.chunk * sizeof(float);
     static uint64_t occ_memo = 0;

@@ -160,6 +160,9 @@ hipError_t launch_attn_pv(hipStream_t st, const AttnDecodeArgs &a);
 // chunks of head h, then forms its partial sums as attn_pv does (identical results). hipErrorInvalidConfiguration
 // when the device cannot hold every chunk block at once (then use attn_scores + attn_pv).
 hipError_t launch_attn_long(hipStream_t st, const AttnDecodeArgs &a, int cu_count);
+// whether launch_attn_long takes this shape (head_dim <= 128, chunks of hd to 256 positions covering ctx); shapes it
+// does not take run on attn_scores + attn_pv
+bool attn_long_ok(const AttnDecodeArgs &a);
 // largest kv the one-kernel attention takes for this shape (0: the shape needs the two-kernel path)
 uint32_t attn_small_limit(const AttnDecodeArgs &a);
 // kv <= kv_max <= min(ctx, attn_small_limit); kv_max sizes the LDS
