@@ -35,7 +35,10 @@ Printed (one JSON line on stdout):
   isolated_kernels  (--config 7b, no --no-isolated; alone with --isolated-only) the isolated operators through the
                public VKLLM_OP_* API: GEMV [1x4096].[4096x11008] and [1x4096].[4096x32000], GEMM
                [512x4096].[4096x4096], RMSNorm [512x4096], RoPE [1,32,512,128]; average launch duration back to back
-               (operands cycled past the 256 MB memory-side cache) and the fraction of the HBM or fp16 MFMA roofline
+               (operands cycled past the 256 MB memory-side cache) and the fraction of the HBM or fp16 MFMA roofline;
+               also one GPU's share of the 7B decode GEMVs if they were split four ways (tensor parallel, design
+               only): the column-parallel [1x4096].[4096x1024] and [1x4096].[4096x2752] and the row-parallel
+               [1x1024].[1024x4096] and [1x2752].[2752x4096]
 """
 import argparse
 import json
@@ -235,11 +238,15 @@ def isolated_kernels(ctx, vk, reps=64):
 
     keep = []
     try:
-        # GEMV [1 x 4096] . [4096 x N] (B stored [N, K], the reference's mat_mul_vec case)
-        x = ctx.tensor_from(normal((1, 1, 1, K)), "x")
-        keep.append(x)
-        for N in (11008, 32000):
-            w = normal((1, 1, N, K))
+        # GEMV [1 x Kx] . [Kx x N] (B stored [N, Kx], the reference's mat_mul_vec case): the 7B widths, then one
+        # GPU's share of the decode GEMVs split four ways (Wq/Wk/Wv and up/gate by output rows, Wo and down by input
+        # columns)
+        for name, N, Kx in (("gemv_1x4096x11008", 11008, K), ("gemv_1x4096x32000", 32000, K),
+                            ("tp4_gemv_1x4096x1024", 1024, K), ("tp4_gemv_1x4096x2752", 2752, K),
+                            ("tp4_gemv_1x1024x4096", 4096, 1024), ("tp4_gemv_1x2752x4096", 4096, 2752)):
+            x = ctx.tensor_from(normal((1, 1, 1, Kx)), "x")
+            keep.append(x)
+            w = normal((1, 1, N, Kx))
             copies = max(1, -(-2 * CACHE_BYTES // w.nbytes))
             ops = []
             for c in range(copies):
@@ -248,10 +255,10 @@ def isolated_kernels(ctx, vk, reps=64):
                 keep += [tw, to]
                 ops.append(to)
             del w
-            timed(f"gemv_1x{K}x{N}", ops, reps, N * K * 2 + K * 2 + N * 2, "GB/s")
-            for t in keep[1:]:
+            timed(name, ops, reps, N * Kx * 2 + Kx * 2 + N * 2, "GB/s")
+            for t in reversed(keep):
                 ctx.free(t)
-            keep = keep[:1]
+            keep = []
         # GEMM [512 x 4096] . [4096 x 4096] (B stored [N, K]): matrix-core bound
         M, N = 512, 4096
         ta = ctx.tensor_from(normal((1, 1, M, K)), "a")
