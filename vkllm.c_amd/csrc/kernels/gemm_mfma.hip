@@ -547,6 +547,12 @@ __global__ __launch_bounds__(256, (PF > 2 ? 1 : PF)) void gemm32_kernel(const ui
 }
 
 // C = epilogue(sum over z of work[z]) for split-K products, the splits added in order
+// whether the plain, SiLU and residual epilogues of the split-K reduce can move 8 columns as one 16-byte vector
+__host__ __device__ __forceinline__ bool reduce_vec8(uint32_t N, uint32_t ldc, uint32_t n_base, const uint16_t *C)
+{
+    return N % 8 == 0 && ldc % 8 == 0 && n_base % 8 == 0 && (uintptr_t)C % 16 == 0;
+}
+
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float *work, uint16_t *C, uint32_t M,
                                                                  uint32_t N, uint32_t ldc, uint32_t split,
@@ -608,6 +614,41 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float *wo
         }
         return;
     }
+    if (reduce_vec8(N, ldc, n_base, C))
+    {
+        // 8 consecutive columns per step: 16-byte partial loads and one 16-byte store (the same sums, in the same
+        // split order, as the element loop below)
+        const uint32_t per_row = N / 8;
+        const uint64_t chunks = (uint64_t)M * per_row;
+        for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < chunks; i += (uint64_t)gridDim.x * 256)
+        {
+            const uint32_t m = (uint32_t)(i / per_row), n = 8 * (uint32_t)(i % per_row);
+            float v[8];
+            sum8((size_t)m * N + n, v);
+            uint16_t *c = C + (size_t)m * ldc + n_base + n;
+            u32x4 o;
+            if constexpr (EPI == GEMM_RESID)
+            {
+                const u32x4 old = *(const u32x4 *)c;
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    o[k] = pack2(f2h(half_lo(old[k]) + h2f(f2h(v[2 * k]))),
+                                 f2h(half_hi(old[k]) + h2f(f2h(v[2 * k + 1]))));
+            }
+            else
+            {
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    if (EPI == GEMM_SILU_HI && n_base + n + k >= split)
+                        v[k] = silu(v[k]);
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    o[k] = pack2(f2h(v[2 * k]), f2h(v[2 * k + 1]));
+            }
+            *(u32x4 *)c = o;
+        }
+        return;
+    }
     for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (uint64_t)gridDim.x * 256)
     {
         float v = 0.f;
@@ -615,6 +656,19 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_kernel(const float *wo
             v += work[(size_t)z * total + i];
         gemm_store(EPI, C, ldc, (uint32_t)(i / N), n_base + (uint32_t)(i % N), v, split);
     }
+}
+
+// work items of gemm_splitk_reduce_kernel: 8 columns each where the epilogue or reduce_vec8 allows, else one element
+template <int EPI>
+static uint32_t reduce_grid(uint32_t M, uint32_t N, uint32_t ldc, uint32_t n_base, const uint16_t *C)
+{
+    uint64_t items = (uint64_t)M * N;
+    if (EPI == GEMM_SWIGLU)
+        items /= 16;
+    else if (EPI == GEMM_QKV_ROPE || reduce_vec8(N, ldc, n_base, C))
+        items /= 8;
+    const uint64_t grid = (items + 255) / 256;
+    return (uint32_t)(grid > 4096 ? 4096 : grid < 1 ? 1 : grid);
 }
 
 // Split-K residual products followed by RMSNorm (every residual product of the token step is): one workgroup per
@@ -798,9 +852,7 @@ template <int EPI>
 static hipError_t launch_reduce(hipStream_t st, const float *work, uint16_t *C, uint32_t M, uint32_t N, uint32_t ldc,
                                 uint32_t split, uint32_t splits, uint32_t n_base, const GemmRope *rope)
 {
-    const uint64_t total = (uint64_t)M * N;
-    uint32_t grid = (uint32_t)((total + 255) / 256);
-    grid = grid > 4096 ? 4096 : grid;
+    const uint32_t grid = reduce_grid<EPI>(M, N, ldc, n_base, C);
     gemm_splitk_reduce_kernel<EPI>
         <<<grid, 256, 0, st>>>(work, C, M, N, ldc, split, splits, n_base, rope ? *rope : GemmRope{});
     return hipGetLastError();
@@ -832,9 +884,7 @@ static hipError_t launch_shape(hipStream_t st, const uint16_t *A, const uint16_t
     hipError_t e = launch_tile<BM, BN, EPI, true>(st, A, B, C, work, M, N, K, ldc, split, splits, kchunk);
     if (e != hipSuccess)
         return e;
-    const uint64_t total = (uint64_t)M * N;
-    uint32_t grid = (uint32_t)((total + 255) / 256);
-    grid = grid > 4096 ? 4096 : grid;
+    const uint32_t grid = reduce_grid<EPI>(M, N, ldc, 0, C);
     gemm_splitk_reduce_kernel<EPI><<<grid, 256, 0, st>>>(work, C, M, N, ldc, split, splits, 0, GemmRope{});
     return hipGetLastError();
 }
