@@ -186,7 +186,9 @@ def test_rmsnorm_needs_f32_weight(ctx, vk):
 # ---------------------------------------------------------------------------------------------------------------
 # ROPE: tests/vkllm_test_op_rope.c; model layout: a [1,S,H,hd] view permuted to [1,H,S,hd]
 @pytest.mark.parametrize("neox", [False, True])
-@pytest.mark.parametrize("S,H,hd,offset", [(512, 32, 128, 0), (16, 6, 48, 0), (1, 32, 128, 383), (3, 4, 64, 4093)])
+# (4, 40, 128, 7): more 16-byte vectors per position (640) than a workgroup requests before its angle table (512)
+@pytest.mark.parametrize("S,H,hd,offset", [(512, 32, 128, 0), (16, 6, 48, 0), (1, 32, 128, 383), (3, 4, 64, 4093),
+                                           (4, 40, 128, 7)])
 def test_rope(ctx, vk, oracle, neox, S, H, hd, offset):
     x = rand((1, 1, S, H * hd), np.float16, -2, 2, seed=7)
     base = ctx.tensor_from(x)

@@ -345,6 +345,27 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(TView in, TView out, uin
     __shared__ float cs[2 * kMaxRopeFreqs];
     const uint32_t h = blockIdx.x, b = blockIdx.y;
     const uint32_t half = in.n[3] / 2, C = in.n[1];
+    const uint16_t *src = (const uint16_t *)in.p;
+    uint16_t *dst = (uint16_t *)out.p;
+    // vectors of the row per channel: 4 adjacent pairs (2w, 2w + 1) each, or with neox 8 pairs (w, w + half) as a
+    // vector of the low half and the matching one of the high half
+    const uint32_t nv = neox ? half / 8 : in.n[3] / 8, items = C * nv;
+    auto at_lo = [&](const TView &t, uint32_t i) { return voff(t, b, i / nv, h, 8 * (i % nv)); };
+    auto at_hi = [&](const TView &t, uint32_t i) { return voff(t, b, i / nv, h, half + 8 * (i % nv)); };
+    // the first kPre items of every thread are requested before the angle table is computed, so their memory
+    // latency overlaps the cosf / sinf work (the isolated [1, 32, 512, 128] operator: all of a workgroup's items)
+    constexpr int kPre = 2;
+    u32x4 plo[kPre], phi[kPre];
+#pragma unroll
+    for (int p = 0; p < kPre; ++p)
+    {
+        const uint32_t i = threadIdx.x + p * blockDim.x;
+        if (i < items)
+        {
+            plo[p] = *(const u32x4 *)(src + at_lo(in, i));
+            phi[p] = neox ? *(const u32x4 *)(src + at_hi(in, i)) : plo[p];
+        }
+    }
     for (uint32_t w = threadIdx.x; w < half; w += blockDim.x)
     {
         const float f = (float)(offset + h) / fr.f[w];
@@ -352,49 +373,46 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(TView in, TView out, uin
         cs[2 * w + 1] = sinf(f);
     }
     __syncthreads();
-    const uint16_t *src = (const uint16_t *)in.p;
-    uint16_t *dst = (uint16_t *)out.p;
-    if (!neox)
-    {
-        // a vector holds 4 adjacent pairs (2w, 2w + 1)
-        const uint32_t nv = in.n[3] / 8;
-        for (uint32_t i = threadIdx.x; i < C * nv; i += blockDim.x)
+    auto rotate = [&](uint32_t i, const u32x4 &lo, const u32x4 &hi) {
+        const uint32_t v = i % nv;
+        if (!neox)
         {
-            const uint32_t c = i / nv, v = i % nv;
-            const u32x4 x = *(const u32x4 *)(src + voff(in, b, c, h, 8 * v));
             u32x4 o;
 #pragma unroll
             for (int k = 0; k < 4; ++k)
             {
                 const uint32_t w = 4 * v + k;
                 const float fc = cs[2 * w], fs = cs[2 * w + 1];
-                const float v0 = half_lo(x[k]), v1 = half_hi(x[k]);
+                const float v0 = half_lo(lo[k]), v1 = half_hi(lo[k]);
                 o[k] = pack2(f2h(fc * v0 - fs * v1), f2h(fs * v0 + fc * v1));
             }
-            *(u32x4 *)(dst + voff(out, b, c, h, 8 * v)) = o;
+            *(u32x4 *)(dst + at_lo(out, i)) = o;
+            return;
         }
-    }
-    else
-    {
-        // pairs (w, w + half): a vector of the low half with the matching vector of the high half, 8 pairs
-        const uint32_t nv = half / 8;
-        for (uint32_t i = threadIdx.x; i < C * nv; i += blockDim.x)
-        {
-            const uint32_t c = i / nv, v = i % nv;
-            const u32x4 lo = *(const u32x4 *)(src + voff(in, b, c, h, 8 * v));
-            const u32x4 hi = *(const u32x4 *)(src + voff(in, b, c, h, half + 8 * v));
-            u32x4 olo, ohi;
+        u32x4 olo, ohi;
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-            {
-                const uint32_t w0 = 8 * v + 2 * k, w1 = w0 + 1;
-                const float a0 = half_lo(lo[k]), b0 = half_lo(hi[k]), a1 = half_hi(lo[k]), b1 = half_hi(hi[k]);
-                olo[k] = pack2(f2h(cs[2 * w0] * a0 - cs[2 * w0 + 1] * b0), f2h(cs[2 * w1] * a1 - cs[2 * w1 + 1] * b1));
-                ohi[k] = pack2(f2h(cs[2 * w0 + 1] * a0 + cs[2 * w0] * b0), f2h(cs[2 * w1 + 1] * a1 + cs[2 * w1] * b1));
-            }
-            *(u32x4 *)(dst + voff(out, b, c, h, 8 * v)) = olo;
-            *(u32x4 *)(dst + voff(out, b, c, h, half + 8 * v)) = ohi;
+        for (int k = 0; k < 4; ++k)
+        {
+            const uint32_t w0 = 8 * v + 2 * k, w1 = w0 + 1;
+            const float a0 = half_lo(lo[k]), b0 = half_lo(hi[k]), a1 = half_hi(lo[k]), b1 = half_hi(hi[k]);
+            olo[k] = pack2(f2h(cs[2 * w0] * a0 - cs[2 * w0 + 1] * b0), f2h(cs[2 * w1] * a1 - cs[2 * w1 + 1] * b1));
+            ohi[k] = pack2(f2h(cs[2 * w0 + 1] * a0 + cs[2 * w0] * b0), f2h(cs[2 * w1 + 1] * a1 + cs[2 * w1] * b1));
         }
+        *(u32x4 *)(dst + at_lo(out, i)) = olo;
+        *(u32x4 *)(dst + at_hi(out, i)) = ohi;
+    };
+#pragma unroll
+    for (int p = 0; p < kPre; ++p)
+    {
+        const uint32_t i = threadIdx.x + p * blockDim.x;
+        if (i < items)
+            rotate(i, plo[p], phi[p]);
+    }
+    for (uint32_t i = threadIdx.x + kPre * blockDim.x; i < items; i += blockDim.x)
+    {
+        const u32x4 lo = *(const u32x4 *)(src + at_lo(in, i));
+        const u32x4 hi = neox ? *(const u32x4 *)(src + at_hi(in, i)) : lo;
+        rotate(i, lo, hi);
     }
 }
 
