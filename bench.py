@@ -25,7 +25,7 @@ Printed (one JSON line on stdout):
                launch / its average duration over back-to-back launches across all layers' weights
   cpu_baseline the C oracle (the CPU restatement of the reference's graph, double accumulation) timing greedy
                decode steps of the full-depth model on the host's cores (at most 16 threads)
-  other_configs  (--config 7b with its own cache length, no --no-companions) the 7b-long and 13b workloads
+  other_configs  (--config 7b with its own cache length, no --no-companions) the 7b-long, 13b and tiny workloads
                measured after the headline one in the same process, through the same C loop and with their own step
                counts whatever --steps says: their decode tok/s, tok/s near positions 1k/2k/4k, prefill ms, and HBM
                roofline fractions
@@ -57,9 +57,14 @@ CACHE_BYTES = 256 << 20  # MI355X memory-side cache: isolated kernels cycle thro
 MODEL_SEED, PROMPT_SEED = 0, 1
 ATTN_SMALL_MAX = 1024  # positions up to which the decode attention is the short-cache kernel (VKLLM_ATTN_SMALL_MAX)
 
+SHAPE_TINY = dict(n_layer=6, dim=288, n_head=6, ffn=768, vocab=32000)
 SHAPE_7B = dict(n_layer=32, dim=4096, n_head=32, ffn=11008, vocab=32000)
 SHAPE_13B = dict(n_layer=40, dim=5120, n_head=40, ffn=13824, vocab=32000)
 CONFIGS = {
+    # launch-latency bound (30 MB of weights a token): its tok/s is reported, not a roofline fraction
+    "tiny": dict(shape=SHAPE_TINY, prompt=16, steps=62, warmup=2, ctx=256, name="tiny LLaMA-2 decoder (dim 288, "
+                 "6 layers, 6 heads of 48, FFN 768, vocab 32000), 16-token prompt prefill then 64 greedy steps at "
+                 "batch 1"),
     "7b": dict(shape=SHAPE_7B, prompt=128, steps=256, warmup=8, ctx=4096, name="LLaMA-2-7B-shaped decoder (dim 4096, "
                "32 layers, 32 heads, FFN 11008, vocab 32000), 128-token prompt prefill then greedy decode at batch 1"),
     "7b-long": dict(shape=SHAPE_7B, prompt=1024, steps=3070, warmup=1, ctx=4096, name="LLaMA-2-7B-shaped decoder, "
@@ -499,7 +504,7 @@ def main():
     others = None
     if not args.no_companions and args.config == "7b" and args.ctx is None:
         others = {}
-        for name in ("7b-long", "13b"):
+        for name in ("7b-long", "13b", "tiny"):
             if name == "13b":
                 model.close()
                 model = None

@@ -475,8 +475,8 @@ static vkllm_err_t ensure_state(vkllm_context *ctx, ModelPriv *mp, uint32_t S)
         fs->argmax_epi = !(am && *am == '0');
         HIP_TRY(hipMalloc(&fs->am_val, kArgmaxCandidates * sizeof(float)));
         HIP_TRY(hipMalloc(&fs->am_idx, kArgmaxCandidates * sizeof(uint32_t)));
-        HIP_TRY(hipMalloc(&fs->am_count, sizeof(uint32_t)));
-        HIP_TRY(hipMemset(fs->am_count, 0, sizeof(uint32_t)));
+        HIP_TRY(hipMalloc(&fs->am_count, vk::kArgmaxSyncWords * sizeof(uint32_t)));
+        HIP_TRY(hipMemset(fs->am_count, 0, vk::kArgmaxSyncWords * sizeof(uint32_t)));
         make_node_records(fs, mp->L);
     }
     if (S > 1 && S <= 128 && !mp->fs->stream_tried)

@@ -76,8 +76,8 @@ enum GemvEpi : int
     EPI_GATEUP = 2, // rows [0,F) up, [F,2F) gate: out[r] = fp16(fp16(up_r) * fp16(silu(gate_r)))
     EPI_QKV = 3,   // rows [0,3D) of [Wq;Wk;Wv]: RoPE on q,k; q -> out, k/v -> caches at step->offset
     // EPI_PLAIN's out, and the arg max of all rows under the reference's order (am_before) into am_ids[0] and
-    // am_io->id: each workgroup publishes its best (value, row), the last to arrive on am_count reduces them and
-    // clears the counter (no workgroup waits for another)
+    // am_io->id: each workgroup publishes its best (value, row), the last to arrive on the am_count counters
+    // reduces them and clears the counters (no workgroup waits for another)
     EPI_ARGMAX = 4,
     EPI_RAW = 5, // EPI_PLAIN's out from the input as given, no RMSNorm (the MATMUL op's mat_mul_vec case)
     // EPI_QKV, then each head's single-token attention (kv = step->offset + 1 <= kAttnTailMaxKv) computed by the
@@ -117,9 +117,11 @@ struct GemvArgs
     DecodeIo *am_io;    // optional
     float *am_val;      // per-workgroup candidates [am_cap]
     uint32_t *am_idx;   // [am_cap]
-    uint32_t *am_count; // arrivals, zero between launches
+    uint32_t *am_count; // arrival counters [kArgmaxSyncWords], zero between launches
     uint32_t am_cap;
 };
+// EPI_ARGMAX arrival counters: kArgmaxCounters first-level words and one top word, each on its own 256 bytes
+constexpr uint32_t kArgmaxCounters = 16, kArgmaxStride = 64, kArgmaxSyncWords = (kArgmaxCounters + 1) * kArgmaxStride;
 hipError_t launch_gemv(hipStream_t st, int epi, const GemvArgs &a, int cu_count);
 
 // Single-token attention over the cache for every head (kv = step->offset + 1): s_j = fp16(scale q.k_j),
