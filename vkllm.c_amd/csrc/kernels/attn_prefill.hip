@@ -64,7 +64,8 @@ __device__ __forceinline__ float row4_sum(float v)
     return v + __shfl_xor(v, 32);
 }
 
-template <int HD>
+// ONE: kv <= 2 key blocks, computed in one pass (below); otherwise the two passes
+template <int HD, bool ONE>
 __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *q, const uint16_t *kc,
                                                                 const uint16_t *vc, uint16_t *out, uint32_t offset,
                                                                 uint32_t S, uint32_t H, uint32_t ctx, float scale,
@@ -179,6 +180,148 @@ __global__ __launch_bounds__(256) void attn_prefill_mfma_kernel(const uint16_t *
     // The wave's rows span positions [pos_lo, pos_hi]: a block wholly before pos_lo (and inside kv) needs no masks,
     // and a block wholly after pos_hi adds nothing to the sums, only to the max.
     const uint32_t pos_lo = offset + min(row0 + wave * 16, S - 1), pos_hi = offset + min(row0 + wave * 16 + 15, S - 1);
+    if constexpr (ONE)
+    {
+        // kv <= 128: every K and V row of the step in one round trip (V blocks 0 and 1 are in flight since entry),
+        // all four tiles in LDS behind one barrier, and each block's scores kept in registers from the statistics to
+        // the probabilities, so nothing is computed twice. The statistics and the probabilities are the arithmetic
+        // of the two passes below (pass 1's step1, pass 2's step2) in the same order, so the outputs are the same
+        // bit for bit.
+        const uint32_t nb = (kv + kPfKeys - 1) / kPfKeys; // 1 or 2 (the launcher's condition)
+        const uint32_t last = offset + min(row0 + kPfRows, S) - 1, nbp = last / kPfKeys + 1;
+        auto store_v1 = [&](auto set_tag, int buf) {
+            constexpr int SI = decltype(set_tag)::value;
+            if (!transposed)
+            {
+#pragma unroll
+                for (int i = 0; i < VP; ++i)
+                {
+                    const uint32_t v = tid + 256 * i, p = v % 32, ch = v / 32;
+                    const uint32_t col = (((p >> 1) ^ ((tid >> 5) & 1u)) << 2) + 2 * (p & 1);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                    {
+                        uint16_t *row = Vt(buf) + (8 * ch + 2 * e) * VROW + col;
+                        *(uint32_t *)row = (vr[SI][i][e] & 0xffffu) | (vr[SI][VP + i][e] << 16);
+                        *(uint32_t *)(row + VROW) = (vr[SI][i][e] >> 16) | (vr[SI][VP + i][e] & 0xffff0000u);
+                    }
+                }
+            }
+            else
+            {
+#pragma unroll
+                for (int i = 0; i < VT; ++i)
+                {
+                    const uint32_t v = tid + 256 * i, n = v / (kPfKeys / 8), c = v % (kPfKeys / 8);
+                    const u32x4 x = vr[SI][i];
+                    *(u32x4 *)(Vt(buf) + n * VROW + 8 * c) = ((tid >> 6) & 1u) ? u32x4{x[2], x[3], x[0], x[1]} : x;
+                }
+            }
+        };
+        load_k(S0{}, 0);
+        load_k(S1{}, kPfKeys);
+        store_k(S0{}, 0);
+        store_k(S1{}, 1);
+        store_v1(S0{}, 0);
+        store_v1(S1{}, 1);
+        __syncthreads();
+        float m = -FLT_MAX, l = 0.f;
+        auto stats = [&](const f32x4a *st, uint32_t jb) {
+            const bool inside = jb + kPfKeys <= kv;
+            float bm = -FLT_MAX;
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (inside || jb + 16 * b + 4 * q4 + e < kv)
+                        bm = fmaxf(bm, st[b][e]);
+            const float mn = fmaxf(m, row4_max(bm));
+            float add = 0.f;
+            if (jb + kPfKeys <= pos_lo + 1)
+            {
+                const float nm = -mn * kLog2e;
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        add += pf_exp2(fmaf(st[b][e], kLog2e, nm));
+            }
+            else if (jb <= pos_hi)
+            {
+                const float nm = -mn * kLog2e;
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (jb + 16 * b + 4 * q4 + e <= pos)
+                            add += pf_exp2(fmaf(st[b][e], kLog2e, nm));
+            }
+            l = l * pf_exp2((m - mn) * kLog2e) + add;
+            m = mn;
+        };
+        f32x4a st0[4], st1[4];
+        scores(0, st0);
+        stats(st0, 0);
+        if (nb > 1)
+        {
+            scores(1, st1);
+            stats(st1, kPfKeys);
+        }
+        const float inv_l = 1.0f / row4_sum(l), nM = -m * kLog2e;
+        f32x4a o[DB];
+#pragma unroll
+        for (int d = 0; d < DB; ++d)
+            o[d] = (f32x4a){0.f, 0.f, 0.f, 0.f};
+        const uint32_t vcol = 4 * (q4 ^ ((c16 >> 3) & 1u));
+        auto pv = [&](const f32x4a *st, int buf, uint32_t jb) {
+            _Float16 ph[4][4];
+            const bool full = jb + kPfKeys <= pos_lo + 1;
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                {
+                    const bool live = full || jb + 16 * b + 4 * q4 + e <= pos;
+                    const uint16_t p = f2h(pf_exp2(fmaf(st[b][e], kLog2e, nM)) * inv_l);
+                    _Float16 f;
+                    __builtin_memcpy(&f, &p, 2);
+                    ph[b][e] = live ? f : (_Float16)0.f;
+                }
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+            {
+                const f16x8a pb = {ph[2 * t][0],     ph[2 * t][1],     ph[2 * t][2],     ph[2 * t][3],
+                                   ph[2 * t + 1][0], ph[2 * t + 1][1], ph[2 * t + 1][2], ph[2 * t + 1][3]};
+#pragma unroll
+                for (int d = 0; d < DB; ++d)
+                {
+                    const uint16_t *vp = Vt(buf) + (16 * d + c16) * VROW + 32 * t + vcol;
+                    const uint2 lo = *(const uint2 *)vp, hi = *(const uint2 *)(vp + 16);
+                    f16x8a a;
+                    const u32x4 w = {lo.x, lo.y, hi.x, hi.y};
+                    __builtin_memcpy(&a, &w, 16);
+                    o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb, o[d], 0, 0, 0);
+                }
+            }
+        };
+        pv(st0, 0, 0);
+        if (nbp > 1)
+            pv(st1, 1, kPfKeys);
+        const uint32_t row = row0 + wave * 16 + c16;
+        if (row < S)
+        {
+            uint16_t *orow = out + (size_t)row * D + (size_t)h * HD;
+#pragma unroll
+            for (int d = 0; d < DB; ++d)
+            {
+                const uint2 w = {pack2(f2h(o[d][0]), f2h(o[d][1])), pack2(f2h(o[d][2]), f2h(o[d][3]))};
+                const uint32_t col = h * HD + 16 * d + 4 * q4;
+                uint16_t *dst = xt ? out + (size_t)xt_vec(row, col / 8) * 8 + col % 8 : orow + 16 * d + 4 * q4;
+                *(uint2 *)dst = w;
+            }
+        }
+        return;
+    }
     float m = -FLT_MAX, l = 0.f;
     const uint32_t nb1 = (kv + kPfKeys - 1) / kPfKeys;
     // kv <= 2 blocks: pass 1 leaves K blocks 0 and 1 in LDS buffers 0 and 1, where pass 2 reads them; otherwise pass
@@ -387,17 +530,17 @@ template <int HD> constexpr size_t pf_lds_bytes()
     return (size_t)2 * (kPfKeys * pf_krow<HD>() + HD * (kPfKeys + 8)) * sizeof(uint16_t);
 }
 
-template <int HD>
+template <int HD, bool ONE>
 static hipError_t launch_pf_hd(hipStream_t st, dim3 grid, const uint16_t *q, const uint16_t *kc, const uint16_t *vc,
                                uint16_t *out, uint32_t offset, uint32_t S, uint32_t H, uint32_t ctx, float scale,
                                bool xt)
 {
     static uint64_t attr_devs = 0; // devices on which the LDS limit is raised for this kernel
     constexpr size_t lds = pf_lds_bytes<HD>();
-    hipError_t e = lds_attr_once((const void *)attn_prefill_mfma_kernel<HD>, lds, attr_devs);
+    hipError_t e = lds_attr_once((const void *)attn_prefill_mfma_kernel<HD, ONE>, lds, attr_devs);
     if (e != hipSuccess)
         return e;
-    attn_prefill_mfma_kernel<HD><<<grid, 256, lds, st>>>(q, kc, vc, out, offset, S, H, ctx, scale, xt);
+    attn_prefill_mfma_kernel<HD, ONE><<<grid, 256, lds, st>>>(q, kc, vc, out, offset, S, H, ctx, scale, xt);
     return hipGetLastError();
 }
 
@@ -413,9 +556,14 @@ hipError_t launch_attn_prefill_mfma(hipStream_t st, const uint16_t *q, const uin
     if (S == 0 || offset + S > ctx || !attn_prefill_mfma_ok(hd) || (xt && S > 128))
         return hipErrorInvalidValue;
     const dim3 grid(H, (S + kPfRows - 1) / kPfRows);
+    // a step whose kv fits two key blocks takes the one-pass form (its own instantiation, so the two-pass kernel's
+    // code and registers are those it has without it)
+    const bool one = offset + S <= 2 * kPfKeys;
     if (hd == 128)
-        return launch_pf_hd<128>(st, grid, q, kc, vc, out, offset, S, H, ctx, scale, xt);
-    return launch_pf_hd<64>(st, grid, q, kc, vc, out, offset, S, H, ctx, scale, xt);
+        return one ? launch_pf_hd<128, true>(st, grid, q, kc, vc, out, offset, S, H, ctx, scale, xt)
+                   : launch_pf_hd<128, false>(st, grid, q, kc, vc, out, offset, S, H, ctx, scale, xt);
+    return one ? launch_pf_hd<64, true>(st, grid, q, kc, vc, out, offset, S, H, ctx, scale, xt)
+               : launch_pf_hd<64, false>(st, grid, q, kc, vc, out, offset, S, H, ctx, scale, xt);
 }
 
 } // namespace vk
